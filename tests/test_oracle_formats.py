@@ -1,0 +1,137 @@
+"""Pins for the oracle's build-defined formats (W4 AWQ-style, GPTQ act-order,
+W8/W4A16 linears, W8A8 int8/fp8) and its fp16/bf16 conversions.  CPU only.
+
+None of these re-types the oracle's formula: each checks an independent
+property (a library conversion, brute-force optimality, a reduction to the
+reference's own gptq_quantize output, exact integer arithmetic, float64
+products)."""
+import numpy as np
+import pytest
+import torch
+
+from helpers import cases
+
+
+def bf16_bits(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, np.uint32) << 16).view(np.float32)
+
+
+def test_f16_and_bf16_conversions_match_libraries(oracle):
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([
+        rng.normal(0, 1, 2000), rng.normal(0, 1e-6, 500), rng.normal(0, 3e4, 500),
+        [0.0, -0.0, 65504, 65519.99, 65520, 1e9, 2.0 ** -24, 2.0 ** -25, 2.0 ** -25 * 1.0001,
+         2.0 ** -14, 2.0 ** -14 * 0.99, 3e-8, np.inf, -np.inf],
+        (np.arange(1, 4000) * 2.0 ** -24) * 1.5,
+    ]).astype(np.float32)
+    want16 = vals.astype(np.float16).view(np.uint16)
+    got16 = np.array([oracle.f32_to_f16(v) for v in vals], np.uint16)
+    assert np.array_equal(got16, want16)
+    back = np.array([oracle.f16_to_f32(h) for h in want16], np.float32)
+    assert np.array_equal(back.view(np.uint32), want16.view(np.float16).astype(np.float32).view(np.uint32))
+    got_b = np.array([oracle.f32_to_bf16(v) for v in vals], np.uint16)
+    assert np.array_equal(got_b, bf16_bits(vals))
+    # W4 scale clamps
+    assert oracle.raw["w4_scale_to_f16"](0.0) == 0x0001
+    assert oracle.raw["w4_scale_to_f16"](1e-30) == 0x0001
+    assert oracle.raw["w4_scale_to_f16"](1e6) == 0x7BFF
+
+
+def test_w4_nibble_order_is_the_reference_int4_byte_order(oracle):
+    # The reference packs element 2i low / 2i+1 high (quantize_int8.c:206-216);
+    # read as little-endian u32, element j sits at bits 4j.  The W4 format uses
+    # exactly that order, so dequantising reference int4 bytes with scale 1 and
+    # zero 0 must give back the reference's unsigned nibbles.
+    rng = np.random.default_rng(4)
+    x = rng.normal(0, 1, 64).astype(np.float32)
+    rc, packed, s = oracle.quantize_int4_sym(x)
+    words = packed.view(np.uint32).reshape(1, 8)
+    scales = np.full((1, 1), 0x3C00, np.uint16)        # 1.0
+    zeros = np.zeros((1, 1), np.uint32)
+    rc, deq = oracle.w4_dequantize(words, scales, zeros, None, 1, 64, 64)
+    nib = np.stack([packed & 0xF, packed >> 4], 1).ravel().astype(np.float32)
+    assert rc == 0 and np.array_equal(deq.ravel(), nib)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_w4_awq_codes_are_nearest_levels(oracle, seed):
+    rng = np.random.default_rng(seed)
+    N, K, g = 24, 512, 128
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[3, :128] = 0.125                                  # constant group -> degenerate path
+    w[4, 128:256] = np.abs(w[4, 128:256]) + 0.01        # all-positive group -> zero clamps to 0
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, g)
+    assert rc == 0
+    nib = ((qw[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, K).astype(np.int64)
+    z = ((qz[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, -1)[:, :K // g].astype(np.int64)
+    s = sc.view(np.float16).astype(np.float32)
+    for n in range(N):
+        for j in range(K // g):
+            wg = w[n, j * g:(j + 1) * g].astype(np.float64)
+            q = nib[n, j * g:(j + 1) * g]
+            if n == 3 and j == 0:
+                assert sc[n, j] == 0x3C00 and z[n, j] == 0 and not q.any()
+                continue
+            lo, hi = wg.min(), wg.max()
+            assert s[n, j] == np.float32(np.float16((np.float32(hi) - np.float32(lo)) / np.float32(15)))
+            levels = (np.arange(16)[None, :] - z[n, j]) * float(s[n, j])
+            err = np.abs(levels - wg[:, None])
+            chosen = err[np.arange(g), q]
+            assert np.all(chosen <= err.min(1) + 1e-6 * float(s[n, j])), (n, j)
+            if 0 < z[n, j] < 15:
+                assert np.all(chosen <= 0.5 * float(s[n, j]) * (1 + 1e-5) + 1e-12)
+
+
+def test_actorder_reduces_to_reference_gptq(oracle, golden):
+    # a21: codes of the act-order format == the reference's gptq_quantize
+    # (bits 4, sym, g 128) run on W[:, stable_argsort(g_idx)]; scales are the
+    # reference's fp32 scales rounded to fp16.
+    f = cases(golden, "actorder")["actorder"]
+    w, g_idx, perm = f["w"], f["g_idx"], f["perm"]
+    N, K = w.shape
+    G = int(g_idx.max()) + 1
+    rc, qw, sc = oracle.w4_gptq_quantize(w, g_idx, G)
+    assert rc == 0
+    nib = ((qw[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(N, K).astype(np.int32)
+    assert np.array_equal(nib[:, perm] - 8, f["q_perm"].astype(np.int32))
+    want_sc = f["s"].astype(np.float16).view(np.uint16)
+    assert np.array_equal(sc, want_sc)
+
+
+def test_linears_against_float64(oracle):
+    rng = np.random.default_rng(5)
+    M, N, K, g = 3, 40, 256, 128
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    xb = bf16_bits(x)
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, g)
+    rc, deq = oracle.w4_dequantize(qw, sc, qz, None, N, K, g)
+    rc, y = oracle.w4a16_linear(xb, qw, sc, qz, None, N, K, g)
+    want = bf16_to_f32(xb).astype(np.float64) @ deq.astype(np.float64).T
+    assert np.abs(y - want).max() <= 1e-5 * np.abs(want).max()
+    # W8 weight-only
+    rc, q, s = oracle.quantize_int8_channel(w)
+    rc, y8 = oracle.w8_linear(x, q, s)
+    want8 = x.astype(np.float64) @ (q.astype(np.float64) * s[:, None].astype(np.float64)).T
+    assert np.abs(y8 - want8).max() <= 1e-5 * np.abs(want8).max()
+    # int8 GEMM accumulators are exact
+    A = rng.integers(-128, 128, (7, 300)).astype(np.int8)
+    B = rng.integers(-128, 128, (9, 300)).astype(np.int8)
+    assert np.array_equal(oracle.i8_gemm_i32(A, B), A.astype(np.int64) @ B.astype(np.int64).T)
+    # fp8 GEMM on decoded operands
+    a = rng.normal(0, 1, (5, 64)).astype(np.float32)
+    b = rng.normal(0, 0.02, (6, 64)).astype(np.float32)
+    _, ca, sa = oracle.quantize_fp8_e4m3_scaled(a)
+    _, cb, sb = oracle.quantize_fp8_e4m3_scaled(b)
+    assert sa == np.float32(np.abs(a).max()) / np.float32(240)
+    out = oracle.fp8_gemm(ca, cb, sa, sb)
+    _, da = oracle.dequantize_fp8(ca.ravel(), "e4m3")
+    _, db = oracle.dequantize_fp8(cb.ravel(), "e4m3")
+    want = (da.reshape(5, 64).astype(np.float64) @ db.reshape(6, 64).astype(np.float64).T) * float(sa) * float(sb)
+    assert np.abs(out - want).max() <= 1e-5 * np.abs(want).max()
+    # codes stay below the reference's field-15 (inf/nan) range when |x/s| <= 240
+    assert ((ca & 0x78) != 0x78).all() and ((cb & 0x78) != 0x78).all()
