@@ -1,0 +1,300 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized linear path on one MI355X.
+
+Headline (BASELINE.json metric, config C2): W4A16 AWQ-style g128 decode GEMV,
+N=11008, K=4096, M=1, bf16 activations, in achieved HBM GB/s of algorithmic
+bytes.  A "step" is one GEMV call; the 16 weight copies rotate so each call
+streams its 23.5 MB from HBM rather than from the 256 MB Infinity Cache.
+
+The JSON line also carries the roofline of the dominant kernel, the CPU
+baseline (the oracle's C restatement on one host core, a bounded sample), and
+`extra` measurements for the other configs (W8A8 int8/fp8 GEMM at M=2048 in
+TOPS, W4A16 at M=4/16, GPTQ act-order, the W8 GEMV).
+
+    python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--no-cpu] [--no-extra]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(REPO, "sneppx-alg_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5033.2        # dense int8 MFMA (256 CU x 8192 op/clk x 2.4 GHz)
+FP8_PEAK_TOPS = 5033.2         # dense fp8 MFMA
+BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
+METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--copies", type=int, default=16, help="rotating weight copies (>256 MB total)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-extra", action="store_true", help="headline config only")
+    p.add_argument("--cpu-seconds", type=float, default=10.0)
+    return p.parse_args()
+
+
+def w4_bytes(M, N, K, G, zeros=True, gidx=False):
+    b = N * K // 2 + N * G * 2 + M * K * 2 + M * N * 2
+    if zeros:
+        b += N * ((G + 7) // 8) * 4
+    if gidx:
+        b += K * 4
+    return b
+
+
+class Timer:
+    """HIP events recorded on the stream the kernels are launched on."""
+
+    def __init__(self, lib, stream):
+        self.lib, self.stream = lib, stream
+
+    def run(self, calls, steps, warmup):
+        import torch
+        for i in range(warmup):
+            calls[i % len(calls)]()
+        torch.cuda.synchronize()
+        # whole-job time: back-to-back launches between two events
+        a, b = self.lib.event(), self.lib.event()
+        self.lib.record(a, self.stream)
+        for i in range(steps):
+            calls[i % len(calls)]()
+        self.lib.record(b, self.stream)
+        total_ms = self.lib.elapsed_ms(a, b)
+        torch.cuda.synchronize()
+        # per-launch duration: an event pair around every launch
+        evs = [(self.lib.event(), self.lib.event()) for _ in range(steps)]
+        for i in range(steps):
+            self.lib.record(evs[i][0], self.stream)
+            calls[i % len(calls)]()
+            self.lib.record(evs[i][1], self.stream)
+        torch.cuda.synchronize()
+        per = sorted(self.lib.elapsed_ms(s, e) for s, e in evs)
+        for s, e in evs:
+            self.lib.fn["snx_hip_event_destroy"](s)
+            self.lib.fn["snx_hip_event_destroy"](e)
+        self.lib.fn["snx_hip_event_destroy"](a)
+        self.lib.fn["snx_hip_event_destroy"](b)
+        return total_ms, sum(per) / len(per), per[len(per) // 2]
+
+
+def make_w4(lib, N, K, group, copies, seed, torch):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    G = K // group
+    qw = torch.empty((N, K // 8), dtype=torch.int32, device="cuda")
+    sc = torch.empty((N, G), dtype=torch.int16, device="cuda")
+    qz = torch.empty((N, (G + 7) // 8), dtype=torch.int32, device="cuda")
+    lib.dev_quantize_w4_awq(w, qw, sc, qz, group)
+    del w
+    return [(qw.clone(), sc.clone(), qz.clone()) for _ in range(copies)], G
+
+
+def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2):
+    ws, G = make_w4(lib, N, K, group, copies, seed, torch)
+    g = torch.Generator(device="cuda").manual_seed(seed + 1)
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    st = timer.stream
+    calls = [lambda c=c: lib.qlinear_w4a16(x, c[0], c[1], c[2], None, G, y, group, stream=st) for c in ws]
+    total, mean_launch, med_launch = timer.run(calls, steps, warmup)
+    nbytes = w4_bytes(M, N, K, G)
+    return {
+        "bytes": nbytes, "ms_per_step": total / steps, "launch_ms_mean": mean_launch,
+        "launch_ms_median": med_launch, "gbs": nbytes / (total / steps) / 1e6,
+        "gbs_kernel": nbytes / mean_launch / 1e6,
+    }, (ws, x, y, G)
+
+
+def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
+    g = torch.Generator(device="cuda").manual_seed(7)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    perm = torch.randperm(K, generator=torch.Generator().manual_seed(7))
+    g_idx = (perm // 128).to(torch.int32).cuda()
+    G = K // 128
+    qw = torch.empty((N, K // 8), dtype=torch.int32, device="cuda")
+    sc = torch.empty((N, G), dtype=torch.int16, device="cuda")
+    lib.dev_quantize_w4_gptq(w, g_idx, G, qw, sc)
+    del w
+    ws = [(qw.clone(), sc.clone()) for _ in range(copies)]
+    x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    st = timer.stream
+    calls = [lambda c=c: lib.qlinear_w4a16(x, c[0], c[1], None, g_idx, G, y, 128, stream=st) for c in ws]
+    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    nbytes = w4_bytes(M, N, K, G, zeros=False, gidx=True)
+    return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
+            "gbs_kernel": nbytes / mean_launch / 1e6}
+
+
+def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
+    g = torch.Generator(device="cuda").manual_seed(11)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    q = torch.empty((N, K), dtype=torch.int8, device="cuda")
+    s = torch.empty(N, device="cuda")
+    lib.dev_quantize_int8_channel(w, q, s)
+    del w
+    ws = [(q.clone(), s.clone()) for _ in range(copies)]
+    x = torch.randn((1, K), device="cuda", generator=g)
+    y = torch.empty((1, N), device="cuda")
+    st = timer.stream
+    calls = [lambda c=c: lib.qlinear_w8_gemv(x, c[0], c[1], y, stream=st) for c in ws]
+    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    nbytes = N * K + N * 4 + K * 4 + N * 4
+    return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
+            "gbs_kernel": nbytes / mean_launch / 1e6}
+
+
+def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
+    g = torch.Generator(device="cuda").manual_seed(13)
+    a32 = torch.randn((M, K), device="cuda", generator=g)
+    w32 = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    st = timer.stream
+    if fp8:
+        A = torch.empty((M, K), dtype=torch.uint8, device="cuda")
+        W = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+        sA, sW = torch.empty(1, device="cuda"), torch.empty(1, device="cuda")
+        lib.dev_quantize_fp8_e4m3_scaled(a32, A, sA)
+        lib.dev_quantize_fp8_e4m3_scaled(w32, W, sW)
+        calls = [lambda: lib.qlinear_w8a8_fp8(A, sA, W, sW, out, stream=st)]
+    else:
+        A = torch.empty((M, K), dtype=torch.int8, device="cuda")
+        W = torch.empty((N, K), dtype=torch.int8, device="cuda")
+        sA, sW = torch.empty(M, device="cuda"), torch.empty(N, device="cuda")
+        lib.dev_quantize_int8_channel(a32, A, sA)
+        lib.dev_quantize_int8_channel(w32, W, sW)
+        calls = [lambda: lib.qlinear_w8a8_i8(A, sA, W, sW, out, stream=st)]
+    del a32, w32
+    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    ops = 2 * M * N * K
+    return {"ops": ops, "ms_per_step": total / steps, "tops": ops / (total / steps) / 1e9,
+            "tops_kernel": ops / mean_launch / 1e9}
+
+
+def cpu_baseline(ws_host, x_host, N, K, group, seconds):
+    """The oracle's C restatement (C2 GEMV: dequantise + k-ascending fp32 dot,
+    the reference tensor.c:1820-1823 order), one host thread, -O3."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(REPO, "oracle"))
+    from py_oracle import Oracle
+    orc = Oracle(perf=True)
+    qw, sc, qz = ws_host
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        orc.w4a16_linear(x_host, qw, sc, qz, None, N, K, group)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= 200:
+            break
+    per = el / reps
+    nbytes = w4_bytes(1, N, K, K // group)
+    return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"full C2 shape N={N} K={K} M=1, {reps} calls in {el:.1f} s "
+                      f"({per * 1e3:.1f} ms/call), oracle/liboracle_perf.so (-O3 -march=x86-64-v3)",
+            "host_cpu": _cpu_name(), "host_threads_available": os.cpu_count()}
+
+
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the quantized GEMV/GEMM "
+                                   "path has no collective step; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+    import sneppx_quant
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    lib = sneppx_quant.load()
+    arch, cus, clk = lib.device_info()
+    stream = torch.cuda.current_stream().cuda_stream
+    timer = Timer(lib, stream)
+
+    N, K, group, M = 11008, 4096, 128, 1
+    head, keep = bench_w4a16(lib, timer, torch, M, N, K, group, args.copies, args.steps, args.warmup)
+    print(f"[bench] C2 M=1: {head['gbs']:.0f} GB/s whole-job, kernel {head['launch_ms_mean'] * 1e3:.2f} us",
+          file=sys.stderr, flush=True)
+
+    extra = []
+    if not args.no_extra:
+        for m in (4, 16):
+            r, _ = bench_w4a16(lib, timer, torch, m, N, K, group, args.copies, max(50, args.steps // 4), 10)
+            extra.append({"workload": f"C2 W4A16 g128 GEMV N={N} K={K} M={m}", "value": round(r["gbs"], 1),
+                          "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                          "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
+        for m in (1, 8):
+            r = bench_w4a16_gptq(lib, timer, torch, m, N, K, args.copies, 20, 3)
+            extra.append({"workload": f"C3 GPTQ act-order W4A16 N={N} K={K} M={m}", "value": round(r["gbs"], 1),
+                          "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                          "ms_per_step": round(r["ms_per_step"], 5)})
+        r = bench_w8(lib, timer, torch, 4096, 4096, 20, max(50, args.steps // 4), 10)
+        extra.append({"workload": "C1 W8 weight-only GEMV N=4096 K=4096 M=1 fp32", "value": round(r["gbs"], 1),
+                      "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                      "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
+        for fp8 in (False, True):
+            r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, 10, 2, fp8=fp8)
+            peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS
+            extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N=14336 K=4096",
+                          "value": round(r["tops"], 1), "unit": "TOPS",
+                          "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4)})
+        torch.cuda.synchronize()
+
+    cpu = None
+    if not args.no_cpu:
+        ws, x, y, G = keep
+        qw, sc, qz = ws[0]
+        import numpy as np
+        host = (qw.cpu().numpy().view(np.uint32), sc.cpu().numpy().view(np.uint16),
+                qz.cpu().numpy().view(np.uint32))
+        xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
+        cpu = cpu_baseline(host, xh, N, K, group, args.cpu_seconds)
+
+    achieved = head["bytes"] / head["launch_ms_mean"] / 1e6
+    line = {
+        "metric": METRIC,
+        "value": round(head["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded torch.randn N(0,0.02) weights quantized on the GPU, N(0,1) bf16 activations)",
+        "config": {"workload": "C2 W4A16 AWQ-style g128 decode GEMV", "N": N, "K": K, "M": M,
+                   "group": group, "weight_copies": args.copies,
+                   "bytes_per_step": head["bytes"], "device": arch, "cus": cus},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_w4a16_gemv", "launch_us_mean": round(head["launch_ms_mean"] * 1e3, 3),
+                     "launch_us_median": round(head["launch_ms_median"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

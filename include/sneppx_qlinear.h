@@ -1,0 +1,110 @@
+/*
+ * sneppx_qlinear.h - device-pointer quantizers and quantized linears (gfx950).
+ *
+ * The reference has no GEMV/GEMM on its quantized path (its linears are fp32
+ * matmuls, kernel/tensor/tensor.c:1753-1828 called from
+ * kernel/attention/attention.c:366-368,433,500-502,584 and
+ * kernel/inference/inference_engine.c:264).  These entry points are the new
+ * MI355X path in the reference's style: plain C types, 0 on success, -1 on
+ * error, caller-allocated outputs.  Unlike the host API in
+ * sneppx_quantization.h, every pointer here is a DEVICE pointer and every call
+ * is asynchronous on `stream` (a hipStream_t; NULL is the default stream).
+ *
+ * Layouts (row-major; W is [N, K], output-major, y = x . W^T as in the
+ * reference's Python QuantizedLinear, bindings/python/.../quantization.py:451):
+ *   W8     qweight int8 [N][K], scales fp32 [N]  (SNEPPX_quantize_int8_channel)
+ *   W4     qweight uint32 [N][K/8], element k at bits 4*(k%8) (the reference's
+ *          int4 nibble order, quantize_int8.c:206-216, read as little-endian
+ *          words); scales fp16 [N][G]; qzeros uint32 [N][ceil(G/8)], group j at
+ *          bits 4*(j%8), or NULL for symmetric codes with implicit zero 8.
+ *          Groups are `group` contiguous columns, or given per column by
+ *          g_idx int32 [K] (GPTQ act-order) with G groups.
+ *   x/y    bf16 (uint16 bit patterns) or fp32 as stated per function.
+ * Failure text: SNEPPX_qlinear_last_error() (thread-local, last failing call).
+ */
+#ifndef SNEPPX_QLINEAR_H
+#define SNEPPX_QLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sneppx_quantization.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* hipStream_t; NULL = default stream */
+typedef void* SNEPPXStream;
+
+/* No reference counterpart: last error of this thread, "" if none. */
+const char* SNEPPX_qlinear_last_error(void);
+
+/* ---- device quantizers (bit-exact with the host API / reference) ------- */
+
+/* Device form of SNEPPX_quantize_int8_channel (quantize_int8.c:157-177):
+ * per-row symmetric int8 with scale max|row|/127.  Used for C1/C4 weights
+ * (per output channel) and C4 activations (per token = per row). */
+int SNEPPX_dev_quantize_int8_channel(const float* in, int8_t* q, float* scales,
+                                     size_t rows, size_t cols, SNEPPXStream stream);
+
+/* W4 AWQ-style asymmetric uint4 (build-defined, generalises
+ * quantize_int8.c:98-123 to 4 bits with a stored fp16 scale):
+ * per (row, group): s = fp16((max-min)/15), z = clamp(roundf(-min/s), 0, 15),
+ * q = clamp(roundf(w/s + z), 0, 15).  K % 8 == 0, K % group == 0. */
+int SNEPPX_dev_quantize_w4_awq(const float* w, uint32_t* qweight, uint16_t* scales,
+                               uint32_t* qzeros, size_t N, size_t K, int group,
+                               SNEPPXStream stream);
+
+/* GPTQ act-order symmetric int4 (build-defined; equals gptq.c:189-239 with
+ * bits 4, sym 1, applied to the columns of each g_idx group in ascending k):
+ * codes c in [-7, 7] stored as c + 8; scale max|w_group|/7 stored as fp16. */
+int SNEPPX_dev_quantize_w4_gptq(const float* w, const int32_t* g_idx, size_t G,
+                                uint32_t* qweight, uint16_t* scales,
+                                size_t N, size_t K, SNEPPXStream stream);
+
+/* Per-tensor scaled FP8 E4M3 with the reference encoder (quantize_fp8.c:41-69):
+ * s = max|x|/240 (1 when below FLT_MIN), code = e4m3(x * (1/s)).  *scale_out
+ * is a device float. */
+int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* scale_out,
+                                        size_t n, SNEPPXStream stream);
+
+/* ---- quantized linears ---------------------------------------------------- */
+
+/* C1: W8 weight-only, fp32 activations: y[m][n] = s[n] * sum_k x[m][k]*q[n][k]
+ * (fp32).  x fp32 [M][K], y fp32 [M][N].  Decode GEMV, HBM-bound. */
+int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* scales,
+                           float* y, size_t M, size_t N, size_t K, SNEPPXStream stream);
+
+/* C2/C3/C5: W4A16.  x bf16 [M][K]; y [M][N] in y_dtype (SNEPPX_BFLOAT16 or
+ * SNEPPX_FLOAT32); fp32 accumulation.  qzeros NULL => symmetric zero 8.
+ * g_idx NULL => contiguous groups of `group` columns; otherwise g_idx[k] in
+ * [0, G).  Small M runs the decode GEMV; large M the MFMA prefill GEMM. */
+int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
+                         const uint32_t* qzeros, const int32_t* g_idx, size_t G,
+                         void* y, SNEPPXDtype y_dtype, size_t M, size_t N, size_t K,
+                         int group, SNEPPXStream stream);
+
+/* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n]), acc = sum_k A*W in
+ * int32 (exact).  A int8 [M][K] (per-token scales sA fp32 [M]), W int8 [N][K]
+ * (per-channel sW fp32 [N]), out bf16 [M][N]. */
+int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W,
+                           const float* sW, uint16_t* out, size_t M, size_t N, size_t K,
+                           SNEPPXStream stream);
+
+/* C4 int8 accumulators only: C int32 [M][N] = A . W^T (for bit-exact checks). */
+int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C,
+                               size_t M, size_t N, size_t K, SNEPPXStream stream);
+
+/* C4 fp8: A, W are reference E4M3 codes (|x/s| < 256 so every code is an
+ * OCP e4m3fn value of equal magnitude); per-tensor scales sA, sW are device
+ * floats; fp32 accumulation; out bf16 [M][N] = bf16((acc * sA) * sW). */
+int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W,
+                            const float* sW, uint16_t* out, size_t M, size_t N, size_t K,
+                            SNEPPXStream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SNEPPX_QLINEAR_H */

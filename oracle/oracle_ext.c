@@ -212,19 +212,44 @@ int orc_w4_dequantize(const uint32_t* qweight, const uint16_t* scales,
     return 0;
 }
 
+/* Row by row: dequantise row n (as orc_w4_dequantize), then the k-ascending
+ * fp32 dot for every m.  Same bits as dequantising W whole and calling
+ * orc_matmul_nk, without the N*K buffer. */
 int orc_w4a16_linear(const uint16_t* x_bf16, const uint32_t* qweight,
                      const uint16_t* scales, const uint32_t* qzeros,
                      const int32_t* g_idx, size_t M, size_t N, size_t K,
                      int group, float* y)
 {
     if (!x_bf16 || !y || M == 0) return -1;
-    float* wd = (float*)malloc(N * K * sizeof(float));
+    float* wd = (float*)malloc(K * sizeof(float));
     float* xf = (float*)malloc(M * K * sizeof(float));
     if (!wd || !xf) { free(wd); free(xf); return -1; }
-    int rc = orc_w4_dequantize(qweight, scales, qzeros, g_idx, N, K, group, wd);
-    if (rc == 0) {
-        for (size_t i = 0; i < M * K; i++) xf[i] = orc_bf16_to_f32(x_bf16[i]);
-        orc_matmul_nk(xf, wd, y, M, K, N);
+    int rc = 0;
+    for (size_t i = 0; i < M * K; i++) xf[i] = orc_bf16_to_f32(x_bf16[i]);
+    size_t G = 0;
+    if (g_idx) {
+        for (size_t k = 0; k < K; k++)
+            if ((size_t)g_idx[k] + 1 > G) G = (size_t)g_idx[k] + 1;
+    }
+    for (size_t n = 0; n < N && rc == 0; n++) {
+        /* dequantise one row through the full-matrix routine's row layout */
+        const uint32_t* qrow = qweight + n * (K / 8);
+        const uint16_t* srow = scales + n * (g_idx ? G : K / (size_t)group);
+        const uint32_t* zrow = NULL;
+        if (qzeros) {
+            size_t gg = g_idx ? G : K / (size_t)group;
+            zrow = qzeros + n * ((gg + 7) / 8);
+        }
+        rc = orc_w4_dequantize(qrow, srow, zrow, g_idx, 1, K, group, wd);
+        for (size_t m = 0; m < M && rc == 0; m++) {
+            const float* xm = xf + m * K;
+            float acc = 0.0f;
+            for (size_t k = 0; k < K; k++) {
+                float p = xm[k] * wd[k];
+                acc = acc + p;
+            }
+            y[m * N + n] = acc;
+        }
     }
     free(wd);
     free(xf);

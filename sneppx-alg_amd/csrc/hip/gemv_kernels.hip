@@ -1,0 +1,284 @@
+// gemv_kernels.hip - decode GEMVs for gfx950 (HBM-bound).
+//
+//  * W8 weight-only (C1): int8 [N][K] x fp32 activations; 16-byte loads per
+//    lane, bytes converted in registers, per-channel scale applied once.
+//  * W4A16 (C2/C3/C5 decode): packed uint4 [N][K/8] x bf16 activations on
+//    v_mfma_f32_16x16x32_bf16.  Nibbles become bf16 (128 + q) with one
+//    and-or per pair; a second MFMA against the broadcast constant
+//    -(128 + z) removes the bias and zero point exactly, so the fp16 group
+//    scale is applied once per 128-column group in fp32.
+//  * A generic W4A16 kernel (any group size, any g_idx, any M) as fallback.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "codec.h"
+#include "../snx_internal.h"
+
+using namespace snx;
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ __forceinline__ u32x4 load16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+
+// ----------------------------------------------------------------- W8 GEMV
+// One wave per R rows; lane l covers bytes [16 l, 16 l + 16) of every
+// 1024-column slice, so a wave load instruction reads 1 KB contiguous.
+template <int R>
+__global__ void __launch_bounds__(256) k_w8_gemv(const float* __restrict__ x,
+                                                 const int8_t* __restrict__ q,
+                                                 const float* __restrict__ s,
+                                                 float* __restrict__ y, int M, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
+    if (n0 >= N) return;
+    for (int m = 0; m < M; m++) {
+        const float* xm = x + (size_t)m * K;
+        float acc[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[r] = 0.0f;
+        for (int k = lane * 16; k < K; k += 1024) {
+            float xv[16];
+#pragma unroll
+            for (int t = 0; t < 16; t += 4) {
+                float4 v = *reinterpret_cast<const float4*>(xm + k + t);
+                xv[t] = v.x; xv[t + 1] = v.y; xv[t + 2] = v.z; xv[t + 3] = v.w;
+            }
+#pragma unroll
+            for (int r = 0; r < R; r++) {
+                int n = n0 + r < N ? n0 + r : N - 1;
+                u32x4 w = load16(q + (size_t)n * K + k);
+#pragma unroll
+                for (int t = 0; t < 16; t++) {
+                    int b = (int)(int8_t)(w[t >> 2] >> (8 * (t & 3)));
+                    acc[r] += xv[t] * (float)b;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            float v = wave_sum(acc[r]);
+            if (lane == 0 && n0 + r < N) y[(size_t)m * N + n0 + r] = s[n0 + r] * v;
+        }
+    }
+}
+
+// Any K: one wave per row, scalar tail.
+__global__ void __launch_bounds__(256) k_w8_gemv_any(const float* __restrict__ x,
+                                                     const int8_t* __restrict__ q,
+                                                     const float* __restrict__ s,
+                                                     float* __restrict__ y, int M, int N, int K) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    for (int m = 0; m < M; m++) {
+        float acc = 0.0f;
+        for (int k = lane; k < K; k += 64) acc += x[(size_t)m * K + k] * (float)q[(size_t)n * K + k];
+        acc = wave_sum(acc);
+        if (lane == 0) y[(size_t)m * N + n] = s[n] * acc;
+    }
+}
+
+// -------------------------------------------------------------- W4A16 GEMV
+// Work: a workgroup owns 16 output columns n and all of K; its 4 waves take
+// one quarter of K each and meet in LDS.  Per 128-column step a lane loads
+// the 16 bytes (32 nibbles) of row n0 + lane%16 at column 32*(lane/16), which
+// feed 4 MFMAs (one packed word each).  MFMA k-slot t of lane group g is
+// column 32 g + 8 j + {0,4,1,5,2,6,3,7}[t] for MFMA j; the activations are
+// permuted the same way with v_perm_b32, so A and B agree on every k.
+template <int MT, bool ZEROS, bool YF32>
+__global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__ x,
+                                                    const uint32_t* __restrict__ qw,
+                                                    const uint16_t* __restrict__ scales,
+                                                    const uint32_t* __restrict__ qz,
+                                                    void* __restrict__ y, int M, int N, int K,
+                                                    int G, int group) {
+    constexpr int CH = 8;                       // steps whose loads are in flight together
+    __shared__ f32x4 red[4][MT][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int nl = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int n = n0 + nl < N ? n0 + nl : N - 1;
+    const int kw = K >> 3, zw = (G + 7) >> 3;
+    const int steps = K >> 9;                   // 128-column steps per wave (K % 512 == 0)
+    const int s0 = wave * steps;
+    const uint32_t* wrow = qw + (size_t)n * kw + kq * 4;
+
+    f32x4 yacc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) yacc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int sc = 0; sc < steps; sc += CH) {
+        u32x4 wv[CH];
+#pragma unroll
+        for (int c = 0; c < CH; c++)
+            if (sc + c < steps) wv[c] = load16(wrow + (s0 + sc + c) * 16);
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            if (sc + c >= steps) break;
+            const int kbase = (s0 + sc + c) * 128;
+            const int g = kbase / group;
+            const float sf = f16_to_f32(scales[(size_t)n * G + g]);
+            uint32_t z = 8;
+            if (ZEROS) z = (qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u;
+            const uint32_t negc = (0xC300u | z) * 0x00010001u;   // bf16 -(128 + z), twice
+            const u32x4 bneg = {negc, negc, negc, negc};
+            f32x4 acc[MT];
+#pragma unroll
+            for (int t = 0; t < MT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t w = wv[c][j];
+                u32x4 b;
+                b[0] = (w & 0x000F000Fu) | 0x43004300u;
+                b[1] = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+                b[2] = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+                b[3] = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+                const bf16x8 bq = __builtin_bit_cast(bf16x8, b);
+                const bf16x8 bz = __builtin_bit_cast(bf16x8, bneg);
+#pragma unroll
+                for (int t = 0; t < MT; t++) {
+                    const int m = t * 16 + nl;
+                    u32x4 a = {0u, 0u, 0u, 0u};
+                    if (m < M) {
+                        const u32x4 xv = load16(x + (size_t)m * K + kbase + kq * 32 + j * 8);
+                        a[0] = __builtin_amdgcn_perm(xv[2], xv[0], 0x05040100u);
+                        a[1] = __builtin_amdgcn_perm(xv[2], xv[0], 0x07060302u);
+                        a[2] = __builtin_amdgcn_perm(xv[3], xv[1], 0x05040100u);
+                        a[3] = __builtin_amdgcn_perm(xv[3], xv[1], 0x07060302u);
+                    }
+                    const bf16x8 av = __builtin_bit_cast(bf16x8, a);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bq, acc[t], 0, 0, 0);
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bz, acc[t], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) yacc[t] += sf * acc[t];
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) red[wave][t][lane] = yacc[t];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        f32x4 v = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
+        if (n0 + nl >= N) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int m = t * 16 + kq * 4 + i;   // MFMA C layout: row 4*(lane/16)+i, col lane%16
+            if (m >= M) continue;
+            if (YF32)
+                reinterpret_cast<float*>(y)[(size_t)m * N + n0 + nl] = v[i];
+            else
+                reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n0 + nl] = f32_to_bf16(v[i]);
+        }
+    }
+}
+
+// Generic W4A16: one wave per output column n, any group layout and M.
+__global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restrict__ x,
+                                                       const uint32_t* __restrict__ qw,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint32_t* __restrict__ qz,
+                                                       const int32_t* __restrict__ g_idx,
+                                                       void* __restrict__ y, int y_f32, int M,
+                                                       int N, int K, int G, int group) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int kw = K >> 3, zw = (G + 7) >> 3;
+    for (int m = 0; m < M; m++) {
+        float acc = 0.0f;
+        for (int wd = lane; wd < kw; wd += 64) {
+            const uint32_t w = qw[(size_t)n * kw + wd];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int k = wd * 8 + t;
+                int g = g_idx ? g_idx[k] : k / group;
+                g = g < 0 ? 0 : (g >= G ? G - 1 : g);   // out-of-range g_idx stays in bounds
+                const int z = qz ? (int)((qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u) : 8;
+                const float deq = (float)((int)((w >> (4 * t)) & 15u) - z) *
+                                  f16_to_f32(scales[(size_t)n * G + g]);
+                acc += bf16_to_f32(x[(size_t)m * K + k]) * deq;
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (y_f32)
+                reinterpret_cast<float*>(y)[(size_t)m * N + n] = acc;
+            else
+                reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(acc);
+        }
+    }
+}
+
+template <int MT>
+int launch_w4a16(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
+                 hipStream_t st) {
+    dim3 grid((N + 15) / 16), block(256);
+    if (qz) {
+        if (y_f32) k_w4a16_gemv<MT, true, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        else k_w4a16_gemv<MT, true, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+    } else {
+        if (y_f32) k_w4a16_gemv<MT, false, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        else k_w4a16_gemv<MT, false, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+    }
+    return snx_launch_check("k_w4a16_gemv");
+}
+
+}  // namespace
+
+extern "C" {
+
+int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
+                  size_t K, void* st) {
+    if (K % 16 == 0) {
+        constexpr int R = 4;
+        size_t waves = (N + R - 1) / R;
+        k_w8_gemv<R><<<(unsigned)((waves + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, (int)M, (int)N, (int)K);
+    } else {
+        k_w8_gemv_any<<<(unsigned)((N + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, (int)M, (int)N, (int)K);
+    }
+    return snx_launch_check("k_w8_gemv");
+}
+
+int snx_w4a16_gemv_supported(size_t M, size_t N, size_t K, int group) {
+    (void)N;
+    return M >= 1 && M <= 64 && K % 512 == 0 && group > 0 && group % 128 == 0 && K % group == 0;
+}
+
+int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                     const uint32_t* qzeros, void* y, int y_f32, size_t M, size_t N, size_t K,
+                     int group, void* st) {
+    const int G = (int)(K / (size_t)group);
+    if (M <= 16)
+        return launch_w4a16<1>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+    if (M <= 32)
+        return launch_w4a16<2>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+    return launch_w4a16<4>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+}
+
+int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                        const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
+                        int y_f32, size_t M, size_t N, size_t K, int group, void* st) {
+    k_w4a16_generic<<<(unsigned)((N + 3) / 4), 256, 0, S(st)>>>(
+        x, qw, scales, qzeros, g_idx, y, y_f32, (int)M, (int)N, (int)K, (int)G, group);
+    return snx_launch_check("k_w4a16_generic");
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+// runtime.hip - the thin C-ABI over the HIP runtime (include/snx_hip.h) and
+// the library's thread-local error text.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "snx_hip.h"
+#include "../snx_internal.h"
+
+namespace {
+thread_local char g_err[512];
+
+int check(hipError_t e, const char* what) {
+    if (e == hipSuccess) return 0;
+    snx_set_error("%s: %s", what, hipGetErrorString(e));
+    return -1;
+}
+
+hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+}  // namespace
+
+extern "C" {
+
+void snx_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+void snx_clear_error(void) { g_err[0] = 0; }
+
+const char* SNEPPX_qlinear_last_error(void) { return g_err; }
+
+int snx_launch_check(const char* kernel) {
+    return check(hipGetLastError(), kernel);
+}
+
+int snx_hip_device_count(int* count) {
+    if (!count) return -1;
+    return check(hipGetDeviceCount(count), "hipGetDeviceCount");
+}
+
+int snx_hip_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return -1;
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 1;
+    return check(hipMalloc(ptr, bytes), "hipMalloc");
+}
+
+int snx_hip_free(void* ptr) { return ptr ? check(hipFree(ptr), "hipFree") : 0; }
+
+int snx_hip_malloc_async(void** ptr, size_t bytes, void* stream) {
+    if (!ptr) return -1;
+    *ptr = nullptr;
+    if (bytes == 0) bytes = 1;
+    return check(hipMallocAsync(ptr, bytes, S(stream)), "hipMallocAsync");
+}
+
+int snx_hip_free_async(void* ptr, void* stream) {
+    return ptr ? check(hipFreeAsync(ptr, S(stream)), "hipFreeAsync") : 0;
+}
+
+int snx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, S(stream)), "hipMemcpyAsync(H2D)");
+}
+
+int snx_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, S(stream)), "hipMemcpyAsync(D2H)");
+}
+
+int snx_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if (bytes == 0) return 0;
+    return check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, S(stream)), "hipMemcpyAsync(D2D)");
+}
+
+int snx_hip_stream_create(void** stream) {
+    if (!stream) return -1;
+    hipStream_t s = nullptr;
+    if (check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate")) return -1;
+    *stream = s;
+    return 0;
+}
+
+int snx_hip_stream_destroy(void* stream) {
+    return stream ? check(hipStreamDestroy(S(stream)), "hipStreamDestroy") : 0;
+}
+
+int snx_hip_stream_sync(void* stream) { return check(hipStreamSynchronize(S(stream)), "hipStreamSynchronize"); }
+
+int snx_hip_device_sync(void) { return check(hipDeviceSynchronize(), "hipDeviceSynchronize"); }
+
+int snx_hip_event_create(void** event) {
+    if (!event) return -1;
+    hipEvent_t e = nullptr;
+    if (check(hipEventCreate(&e), "hipEventCreate")) return -1;
+    *event = e;
+    return 0;
+}
+
+int snx_hip_event_destroy(void* event) {
+    return event ? check(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy") : 0;
+}
+
+int snx_hip_event_record(void* event, void* stream) {
+    return check(hipEventRecord(reinterpret_cast<hipEvent_t>(event), S(stream)), "hipEventRecord");
+}
+
+int snx_hip_event_sync(void* event) {
+    return check(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+
+int snx_hip_event_elapsed_ms(float* ms, void* start, void* stop) {
+    if (!ms) return -1;
+    return check(hipEventElapsedTime(ms, reinterpret_cast<hipEvent_t>(start),
+                                     reinterpret_cast<hipEvent_t>(stop)), "hipEventElapsedTime");
+}
+
+int snx_hip_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz) {
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return -1;
+    hipDeviceProp_t p;
+    if (check(hipGetDeviceProperties(&p, dev), "hipGetDeviceProperties")) return -1;
+    if (arch && arch_len) {
+        strncpy(arch, p.gcnArchName, arch_len - 1);
+        arch[arch_len - 1] = 0;
+    }
+    if (cu_count) *cu_count = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    return 0;
+}
+
+}  // extern "C"

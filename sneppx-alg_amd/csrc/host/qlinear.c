@@ -1,0 +1,153 @@
+/*
+ * qlinear.c - device-pointer entry points (include/sneppx_qlinear.h):
+ * argument checks, shape dispatch and workspace, then the HIP launchers.
+ * Nothing here touches tensor data; every call is asynchronous on `stream`.
+ */
+#include <stdint.h>
+#include <stdlib.h>
+
+#include "sneppx_qlinear.h"
+#include "snx_hip.h"
+#include "../snx_internal.h"
+
+static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+#define REQUIRE(cond, ...)               \
+    do {                                 \
+        if (!(cond)) {                   \
+            snx_set_error(__VA_ARGS__);  \
+            return -1;                   \
+        }                                \
+    } while (0)
+
+int SNEPPX_dev_quantize_int8_channel(const float* in, int8_t* q, float* scales, size_t rows,
+                                     size_t cols, SNEPPXStream stream) {
+    REQUIRE(in && q && scales, "dev_quantize_int8_channel: NULL pointer");
+    REQUIRE(rows && cols, "dev_quantize_int8_channel: empty matrix");
+    snx_clear_error();
+    return snx_k_quant_int8_rows(in, q, scales, rows, cols, stream);
+}
+
+int SNEPPX_dev_quantize_w4_awq(const float* w, uint32_t* qweight, uint16_t* scales,
+                               uint32_t* qzeros, size_t N, size_t K, int group,
+                               SNEPPXStream stream) {
+    REQUIRE(w && qweight && scales && qzeros, "dev_quantize_w4_awq: NULL pointer");
+    REQUIRE(N && K, "dev_quantize_w4_awq: empty matrix");
+    REQUIRE(group > 0 && group % 8 == 0 && K % (size_t)group == 0,
+            "dev_quantize_w4_awq: group %d must be a positive multiple of 8 dividing K=%zu",
+            group, K);
+    snx_clear_error();
+    return snx_k_w4_awq_quantize(w, qweight, scales, qzeros, N, K, group, stream);
+}
+
+/* g_idx is checked on the host (one small copy) so the kernel's LDS indexing
+ * by group stays in bounds. */
+int SNEPPX_dev_quantize_w4_gptq(const float* w, const int32_t* g_idx, size_t G,
+                                uint32_t* qweight, uint16_t* scales, size_t N, size_t K,
+                                SNEPPXStream stream) {
+    REQUIRE(w && g_idx && qweight && scales, "dev_quantize_w4_gptq: NULL pointer");
+    REQUIRE(N && K && G, "dev_quantize_w4_gptq: empty shape");
+    REQUIRE(K % 8 == 0, "dev_quantize_w4_gptq: K=%zu must be a multiple of 8", K);
+    snx_clear_error();
+    int32_t* h = (int32_t*)malloc(K * sizeof(int32_t));
+    REQUIRE(h, "dev_quantize_w4_gptq: out of host memory");
+    int rc = snx_hip_memcpy_d2h(h, g_idx, K * sizeof(int32_t), stream);
+    if (rc == 0) rc = snx_hip_stream_sync(stream);
+    for (size_t k = 0; rc == 0 && k < K; k++)
+        if (h[k] < 0 || (size_t)h[k] >= G) {
+            snx_set_error("dev_quantize_w4_gptq: g_idx[%zu]=%d outside [0, %zu)", k, h[k], G);
+            rc = -1;
+        }
+    free(h);
+    if (rc) return -1;
+    return snx_k_w4_gptq_quantize(w, g_idx, G, qweight, scales, N, K, stream);
+}
+
+int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* scale_out,
+                                        size_t n, SNEPPXStream stream) {
+    REQUIRE(in && out && scale_out, "dev_quantize_fp8_e4m3_scaled: NULL pointer");
+    REQUIRE(n, "dev_quantize_fp8_e4m3_scaled: n == 0");
+    snx_clear_error();
+    int parts = snx_reduce_parts(n);
+    float* ws = NULL;
+    if (snx_hip_malloc_async((void**)&ws, ((size_t)parts * 2 + 64) * sizeof(float), stream))
+        return -1;
+    float* rec = ws + (size_t)parts * 2;
+    rec = (float*)(((uintptr_t)rec + 15u) & ~(uintptr_t)15u);
+    int rc = snx_k_absmax(in, n, ws, parts, stream);
+    if (!rc) rc = snx_k_finalize_scale(ws, parts, SNX_SCALE_FP8_240, in, rec, scale_out, stream);
+    if (!rc) rc = snx_k_fp8_encode(in, out, n, 0, rec, stream);
+    if (snx_hip_free_async(ws, stream)) rc = -1;
+    return rc;
+}
+
+int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* scales, float* y,
+                           size_t M, size_t N, size_t K, SNEPPXStream stream) {
+    REQUIRE(x && qweight && scales && y, "qlinear_w8_gemv: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w8_gemv: empty shape");
+    REQUIRE(K % 16 != 0 || (aligned16(x) && aligned16(qweight)),
+            "qlinear_w8_gemv: x and qweight must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_w8_gemv(x, qweight, scales, y, M, N, K, stream);
+}
+
+int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
+                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
+                         SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
+                         SNEPPXStream stream) {
+    REQUIRE(x && qweight && scales && y, "qlinear_w4a16: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w4a16: empty shape");
+    REQUIRE(K % 8 == 0, "qlinear_w4a16: K=%zu must be a multiple of 8", K);
+    REQUIRE(y_dtype == SNEPPX_BFLOAT16 || y_dtype == SNEPPX_FLOAT32,
+            "qlinear_w4a16: y_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32");
+    int y_f32 = y_dtype == SNEPPX_FLOAT32;
+    if (g_idx) {
+        REQUIRE(G > 0, "qlinear_w4a16: G must be > 0 with g_idx");
+    } else {
+        REQUIRE(group > 0 && K % (size_t)group == 0,
+                "qlinear_w4a16: group %d must divide K=%zu", group, K);
+        G = K / (size_t)group;
+    }
+    snx_clear_error();
+    if (!g_idx && aligned16(x) && aligned16(qweight) &&
+        snx_w4a16_gemv_supported(M < 64 ? M : 64, N, K, group)) {
+        /* decode GEMV; larger M in 64-row slices that reuse each weight load */
+        size_t ob = y_f32 ? 4 : 2;
+        for (size_t m0 = 0; m0 < M; m0 += 64) {
+            size_t mm = M - m0 < 64 ? M - m0 : 64;
+            if (snx_k_w4a16_gemv(x + m0 * K, qweight, scales, qzeros, (char*)y + m0 * N * ob,
+                                 y_f32, mm, N, K, group, stream))
+                return -1;
+        }
+        return 0;
+    }
+    return snx_k_w4a16_generic(x, qweight, scales, qzeros, g_idx, G, y, y_f32, M, N, K, group,
+                               stream);
+}
+
+int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,
+                           uint16_t* out, size_t M, size_t N, size_t K, SNEPPXStream stream) {
+    REQUIRE(A && sA && W && sW && out, "qlinear_w8a8_i8: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w8a8_i8: empty shape");
+    REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_i8: A and W must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_i8_gemm(A, W, sA, sW, NULL, out, M, N, K, stream);
+}
+
+int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C, size_t M, size_t N,
+                               size_t K, SNEPPXStream stream) {
+    REQUIRE(A && W && C, "qlinear_i8_gemm_i32: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_i8_gemm_i32: empty shape");
+    REQUIRE(aligned16(A) && aligned16(W), "qlinear_i8_gemm_i32: A and W must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_i8_gemm(A, W, NULL, NULL, C, NULL, M, N, K, stream);
+}
+
+int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W, const float* sW,
+                            uint16_t* out, size_t M, size_t N, size_t K, SNEPPXStream stream) {
+    REQUIRE(A && sA && W && sW && out, "qlinear_w8a8_fp8: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w8a8_fp8: empty shape");
+    REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_fp8: A and W must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_fp8_gemm(A, W, sA, sW, out, M, N, K, stream);
+}

@@ -1,0 +1,96 @@
+/*
+ * snx_internal.h - C-ABI between the C host layer and the HIP translation
+ * units of libsneppx_quant.so (not installed; the public surface is in
+ * include/).  Launchers take device pointers and a hipStream_t (as void*),
+ * enqueue their kernels and return 0, or -1 with the error text set.
+ */
+#ifndef SNX_INTERNAL_H
+#define SNX_INTERNAL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+void snx_set_error(const char* fmt, ...);
+void snx_clear_error(void);
+int snx_launch_check(const char* kernel);
+
+/* kinds of snx_k_finalize_scale */
+enum {
+    SNX_SCALE_SYM127 = 0,   /* int8 sym: max/127 (quantize_int8.c:52-59) */
+    SNX_SCALE_SYM7 = 1,     /* int4 sym: max/7   (quantize_int8.c:198-205) */
+    SNX_SCALE_ASYM255 = 2,  /* int8 asym: (max-min)/255, zp (quantize_int8.c:102-117) */
+    SNX_SCALE_FP8_240 = 3   /* per-tensor fp8: max/240 (build-defined) */
+};
+
+/* Scale record written by snx_k_finalize_scale (device memory, 4 floats):
+ * [0] scale, [1] 1/scale, [2] zero point (as float), [3] 1.0 if degenerate. */
+#define SNX_SCALE_REC 4
+
+/* number of partial blocks the reduction launchers use for n elements */
+int snx_reduce_parts(size_t n);
+
+int snx_k_absmax(const float* x, size_t n, float* part, int nparts, void* stream);
+int snx_k_minmax(const float* x, size_t n, float* part, int nparts, void* stream);
+int snx_k_finalize_scale(const float* part, int nparts, int kind, const float* x,
+                         float* rec, float* scale_out, void* stream);
+
+int snx_k_quant_int8_sym(const float* x, int8_t* q, size_t n, const float* rec, void* stream);
+int snx_k_dequant_int8_sym(const int8_t* q, float* y, size_t n, float scale, void* stream);
+int snx_k_quant_int8_asym(const float* x, int8_t* q, size_t n, const float* rec, void* stream);
+int snx_k_dequant_int8_asym(const int8_t* q, float* y, size_t n, float scale, int32_t zp,
+                            void* stream);
+int snx_k_quant_int4_sym(const float* x, uint8_t* p, size_t n, const float* rec, void* stream);
+int snx_k_dequant_int4_sym(const uint8_t* p, float* y, size_t n, float scale, void* stream);
+/* fmt 0 = E4M3, 1 = E5M2; rec == NULL encodes x as is, else x * rec[1] */
+int snx_k_fp8_encode(const float* x, uint8_t* c, size_t n, int fmt, const float* rec,
+                     void* stream);
+int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* stream);
+
+int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
+                          void* stream);
+int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,
+                       size_t group, void* stream);
+/* q may be NULL (bits > 8 store no codes); zeros may be NULL */
+int snx_k_gptq_quantize(const float* w, int8_t* q, float* scales, int32_t* zeros,
+                        size_t rows, size_t cols, size_t group, int bits, int sym,
+                        void* stream);
+int snx_k_awq_scale_weights(float* w, const float* act, float* scale_out, size_t rows,
+                            size_t cols, void* stream);
+int snx_k_gptq_hessian(float* h, const float* act, size_t n, size_t dim, void* stream);
+/* out[0] = scale, out[1] = zero (int32 bits) */
+int snx_k_gptq_block(float* w, const float* h_inv, float* qw, float* out, size_t n,
+                     int bits, int sym, void* stream);
+
+int snx_k_w4_awq_quantize(const float* w, uint32_t* qw, uint16_t* scales, uint32_t* qzeros,
+                          size_t N, size_t K, int group, void* stream);
+int snx_k_w4_gptq_quantize(const float* w, const int32_t* g_idx, size_t G, uint32_t* qw,
+                           uint16_t* scales, size_t N, size_t K, void* stream);
+
+/* ---- linears (gemv_kernels.hip, gemm_kernels.hip) ---- */
+int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y,
+                  size_t M, size_t N, size_t K, void* stream);
+/* y_f32: 1 -> fp32 output, 0 -> bf16 */
+int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                     const uint32_t* qzeros, void* y, int y_f32, size_t M, size_t N,
+                     size_t K, int group, void* stream);
+/* any group size / g_idx, any M: reference-layout fallback */
+int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                        const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
+                        int y_f32, size_t M, size_t N, size_t K, int group, void* stream);
+int snx_w4a16_gemv_supported(size_t M, size_t N, size_t K, int group);
+
+int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
+                  int32_t* c_i32, uint16_t* out_bf16, size_t M, size_t N, size_t K,
+                  void* stream);
+int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const float* sW,
+                   uint16_t* out_bf16, size_t M, size_t N, size_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,324 @@
+"""Python access to libsneppx_quant.so (the HIP-backed quantized linear path).
+
+Two layers, both thin ctypes bindings over the C-ABI in include/:
+
+* `Library` - the reference's host-pointer quantization API
+  (include/sneppx_quantization.h) with numpy in / numpy out, mirroring the
+  return tuples of the reference's C functions (rc first, then outputs).
+* device entry points (include/sneppx_qlinear.h) taking torch tensors that
+  live on the GPU; they launch on torch's current stream unless a stream is
+  given.  torch is only the allocator/stream plumbing here.
+
+There is no fallback: if the shared library is missing, `load()` raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+try:  # torch first: its libamdhip64 must be the one the library binds to
+    import torch
+except ImportError:  # pragma: no cover - torch is part of the image
+    torch = None
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsneppx_quant.so")
+
+# SNEPPXDtype ordinals (multidimensional_tensor_engine.h:27-41)
+SNEPPX_FLOAT32 = 0
+SNEPPX_FLOAT16 = 2
+SNEPPX_BFLOAT16 = 3
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C")
+_i8p = np.ctypeslib.ndpointer(np.int8, flags="C")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C")
+_sz = C.c_size_t
+_vp = C.c_void_p
+
+EXPORTS = {
+    # reference surface
+    "SNEPPX_quantize_int8_sym": (C.c_int, [_f32p, _i8p, _sz, C.POINTER(C.c_float)]),
+    "SNEPPX_dequantize_int8_sym": (C.c_int, [_i8p, _f32p, _sz, C.c_float]),
+    "SNEPPX_quantize_int8_asym": (C.c_int, [_f32p, _i8p, _sz, C.POINTER(C.c_float), C.POINTER(C.c_int32)]),
+    "SNEPPX_dequantize_int8_asym": (C.c_int, [_i8p, _f32p, _sz, C.c_float, C.c_int32]),
+    "SNEPPX_quantize_int8_channel": (C.c_int, [_f32p, _i8p, _sz, _sz, _f32p]),
+    "SNEPPX_quantize_int4_sym": (C.c_int, [_f32p, _u8p, _sz, C.POINTER(C.c_float)]),
+    "SNEPPX_dequantize_int4_sym": (C.c_int, [_u8p, _f32p, _sz, C.c_float]),
+    "SNEPPX_float_to_fp8_e4m3": (C.c_uint8, [C.c_float]),
+    "SNEPPX_fp8_e4m3_to_float": (C.c_float, [C.c_uint8]),
+    "SNEPPX_quantize_fp8_e4m3": (C.c_int, [_f32p, _u8p, _sz]),
+    "SNEPPX_dequantize_fp8_e4m3": (C.c_int, [_u8p, _f32p, _sz]),
+    "SNEPPX_float_to_fp8_e5m2": (C.c_uint8, [C.c_float]),
+    "SNEPPX_fp8_e5m2_to_float": (C.c_float, [C.c_uint8]),
+    "SNEPPX_quantize_fp8_e5m2": (C.c_int, [_f32p, _u8p, _sz]),
+    "SNEPPX_dequantize_fp8_e5m2": (C.c_int, [_u8p, _f32p, _sz]),
+    "SNEPPX_awq_scale_weights": (C.c_int, [_f32p, _sz, _sz, _f32p, _f32p]),
+    "SNEPPX_awq_quantize": (C.c_int, [_f32p, _i8p, _vp, _f32p, _sz, _sz, C.c_int]),
+    "SNEPPX_gptq_quantize": (C.c_int, [_f32p, _sz, _sz, C.c_int, C.c_int, _i8p, _f32p, _vp, C.c_int]),
+    "SNEPPX_gptq_compute_hessian": (C.c_int, [_f32p, _f32p, _sz, _sz]),
+    "SNEPPX_gptq_quantize_block": (C.c_int, [_f32p, _f32p, _f32p, C.POINTER(C.c_float),
+                                             C.POINTER(C.c_int32), _sz, C.c_int, C.c_int]),
+    "SNEPPX_quant_params_create": (C.c_int, [_vp, C.c_int]),
+    "SNEPPX_quant_mode_name": (C.c_char_p, [C.c_int]),
+    # device entry points
+    "SNEPPX_qlinear_last_error": (C.c_char_p, []),
+    "SNEPPX_dev_quantize_int8_channel": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_dev_quantize_w4_awq": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
+    "SNEPPX_dev_quantize_w4_gptq": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_dev_quantize_fp8_e4m3_scaled": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "SNEPPX_qlinear_w8_gemv": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w4a16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, C.c_int, _sz, _sz, _sz,
+                                       C.c_int, _vp]),
+    "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    # thin HIP ABI
+    "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
+    "snx_hip_event_destroy": (C.c_int, [_vp]),
+    "snx_hip_event_record": (C.c_int, [_vp, _vp]),
+    "snx_hip_event_sync": (C.c_int, [_vp]),
+    "snx_hip_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _vp, _vp]),
+    "snx_hip_stream_sync": (C.c_int, [_vp]),
+    "snx_hip_device_info": (C.c_int, [C.c_char_p, _sz, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+}
+
+
+class QuantParams(C.Structure):
+    """SNEPPXQuantParams (quantization.h:42-48)."""
+    _fields_ = [("scale", C.c_float), ("zero_point", C.c_int32), ("qmin", C.c_float),
+                ("qmax", C.c_float), ("scale_max", C.c_float)]
+
+
+class SneppxError(RuntimeError):
+    pass
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    return C.c_void_p(t.data_ptr())
+
+
+class Library:
+    """ctypes view of libsneppx_quant.so."""
+
+    def __init__(self, path: str = LIB_PATH):
+        if not os.path.exists(path):
+            raise SneppxError(f"{path} is not built; run `make -C sneppx-alg_amd` "
+                              "(or __graft_entry__.build()) - there is no CPU fallback")
+        self.path = path
+        self.lib = C.CDLL(path)
+        self.fn = {}
+        for name, (res, args) in EXPORTS.items():
+            f = getattr(self.lib, name)
+            f.restype, f.argtypes = res, args
+            self.fn[name] = f
+
+    def last_error(self) -> str:
+        return self.fn["SNEPPX_qlinear_last_error"]().decode()
+
+    def check(self, rc: int, what: str) -> None:
+        if rc != 0:
+            raise SneppxError(f"{what} failed: {self.last_error()}")
+
+    # ---------------- reference host API (numpy) -------------------------
+    def quantize_int8_sym(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        q = np.zeros(x.size, np.int8)
+        s = C.c_float(0)
+        rc = self.fn["SNEPPX_quantize_int8_sym"](x, q, x.size, C.byref(s))
+        return rc, q, np.float32(s.value)
+
+    def dequantize_int8_sym(self, q, scale):
+        q = np.ascontiguousarray(q, np.int8).ravel()
+        y = np.zeros(q.size, np.float32)
+        return self.fn["SNEPPX_dequantize_int8_sym"](q, y, q.size, scale), y
+
+    def quantize_int8_asym(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        q = np.zeros(x.size, np.int8)
+        s, z = C.c_float(0), C.c_int32(0)
+        rc = self.fn["SNEPPX_quantize_int8_asym"](x, q, x.size, C.byref(s), C.byref(z))
+        return rc, q, np.float32(s.value), int(z.value)
+
+    def dequantize_int8_asym(self, q, scale, zp):
+        q = np.ascontiguousarray(q, np.int8).ravel()
+        y = np.zeros(q.size, np.float32)
+        return self.fn["SNEPPX_dequantize_int8_asym"](q, y, q.size, scale, zp), y
+
+    def quantize_int8_channel(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        rows, cols = x.shape
+        q = np.zeros((rows, cols), np.int8)
+        s = np.zeros(rows, np.float32)
+        rc = self.fn["SNEPPX_quantize_int8_channel"](x, q, rows, cols, s)
+        return rc, q, s
+
+    def quantize_int4_sym(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        p = np.zeros((x.size + 1) // 2, np.uint8)
+        s = C.c_float(0)
+        rc = self.fn["SNEPPX_quantize_int4_sym"](x, p, x.size, C.byref(s))
+        return rc, p, np.float32(s.value)
+
+    def dequantize_int4_sym(self, packed, n, scale):
+        packed = np.ascontiguousarray(packed, np.uint8)
+        y = np.zeros(n, np.float32)
+        return self.fn["SNEPPX_dequantize_int4_sym"](packed, y, n, scale), y
+
+    def quantize_fp8(self, x, fmt="e4m3"):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        c = np.zeros(x.size, np.uint8)
+        return self.fn[f"SNEPPX_quantize_fp8_{fmt}"](x, c, x.size), c
+
+    def dequantize_fp8(self, c, fmt="e4m3"):
+        c = np.ascontiguousarray(c, np.uint8).ravel()
+        y = np.zeros(c.size, np.float32)
+        return self.fn[f"SNEPPX_dequantize_fp8_{fmt}"](c, y, c.size), y
+
+    def awq_scale_weights(self, w, act_scales):
+        w = np.array(w, np.float32, order="C", copy=True)
+        rows, cols = w.shape
+        s = np.zeros((rows, cols), np.float32)
+        a = np.ascontiguousarray(act_scales, np.float32)
+        rc = self.fn["SNEPPX_awq_scale_weights"](w, rows, cols, a, s)
+        return rc, w, s
+
+    def awq_quantize(self, w, group_size, act_scales=None):
+        w = np.ascontiguousarray(w, np.float32)
+        rows, cols = w.shape
+        g = group_size if group_size > 0 else 128
+        q = np.zeros((rows, cols), np.int8)
+        s = np.zeros((rows, (cols + g - 1) // g), np.float32)
+        a = None if act_scales is None else np.ascontiguousarray(act_scales, np.float32)
+        rc = self.fn["SNEPPX_awq_quantize"](w, q, None if a is None else a.ctypes.data_as(_vp),
+                                            s, rows, cols, group_size)
+        return rc, q, s
+
+    def gptq_compute_hessian(self, act):
+        act = np.ascontiguousarray(act, np.float32)
+        n, dim = act.shape
+        h = np.zeros((dim, dim), np.float32)
+        return self.fn["SNEPPX_gptq_compute_hessian"](h, act, n, dim), h
+
+    def gptq_quantize_block(self, w, h_inv, bits, sym):
+        w = np.array(w, np.float32, order="C", copy=True)
+        h = np.array(h_inv, np.float32, order="C", copy=True)
+        qw = np.zeros(w.size, np.float32)
+        s, z = C.c_float(0), C.c_int32(-7)
+        rc = self.fn["SNEPPX_gptq_quantize_block"](w, h, qw, C.byref(s), C.byref(z), w.size, bits, sym)
+        return rc, w, qw, np.float32(s.value), int(z.value)
+
+    def gptq_quantize(self, w, group_size, bits, sym, with_zeros=True):
+        w = np.array(w, np.float32, order="C", copy=True)
+        rows, cols = w.shape
+        g = group_size if group_size > 0 else 128
+        ng = (cols + g - 1) // g
+        q = np.full((rows, cols), 0x55, np.int8)
+        s = np.zeros((rows, ng), np.float32)
+        z = np.full((rows, ng), -7, np.int32) if with_zeros else None
+        rc = self.fn["SNEPPX_gptq_quantize"](w, rows, cols, group_size, bits, q, s,
+                                             None if z is None else z.ctypes.data_as(_vp), sym)
+        return rc, w, q, s, z
+
+    def quant_params_create(self, mode):
+        p = QuantParams()
+        rc = self.fn["SNEPPX_quant_params_create"](C.cast(C.pointer(p), _vp), mode)
+        return rc, (p.scale, p.zero_point, p.qmin, p.qmax, p.scale_max)
+
+    def quant_mode_name(self, mode):
+        return self.fn["SNEPPX_quant_mode_name"](mode).decode()
+
+    # ---------------- device entry points (torch tensors on the GPU) -------
+    @staticmethod
+    def _stream(stream):
+        if stream is not None:
+            return C.c_void_p(stream)
+        return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def dev_quantize_int8_channel(self, w, q, scales, stream=None):
+        rows, cols = w.shape
+        self.check(self.fn["SNEPPX_dev_quantize_int8_channel"](
+            _ptr(w), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)), "dev_quantize_int8_channel")
+
+    def dev_quantize_w4_awq(self, w, qweight, scales, qzeros, group, stream=None):
+        N, K = w.shape
+        self.check(self.fn["SNEPPX_dev_quantize_w4_awq"](
+            _ptr(w), _ptr(qweight), _ptr(scales), _ptr(qzeros), N, K, group, self._stream(stream)),
+            "dev_quantize_w4_awq")
+
+    def dev_quantize_w4_gptq(self, w, g_idx, G, qweight, scales, stream=None):
+        N, K = w.shape
+        self.check(self.fn["SNEPPX_dev_quantize_w4_gptq"](
+            _ptr(w), _ptr(g_idx), G, _ptr(qweight), _ptr(scales), N, K, self._stream(stream)),
+            "dev_quantize_w4_gptq")
+
+    def dev_quantize_fp8_e4m3_scaled(self, x, out, scale, stream=None):
+        self.check(self.fn["SNEPPX_dev_quantize_fp8_e4m3_scaled"](
+            _ptr(x), _ptr(out), _ptr(scale), x.numel(), self._stream(stream)), "dev_quantize_fp8_e4m3_scaled")
+
+    def qlinear_w8_gemv(self, x, qweight, scales, y, stream=None):
+        M, K = x.shape
+        N = qweight.shape[0]
+        self.check(self.fn["SNEPPX_qlinear_w8_gemv"](
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(y), M, N, K, self._stream(stream)), "qlinear_w8_gemv")
+
+    def qlinear_w4a16(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None):
+        M, K = x.shape
+        N = qweight.shape[0]
+        ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_w4a16"](
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(y), ydt,
+            M, N, K, group, self._stream(stream)), "qlinear_w4a16")
+
+    def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None):
+        M, K = A.shape
+        N = W.shape[0]
+        self.check(self.fn["SNEPPX_qlinear_w8a8_i8"](
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), M, N, K, self._stream(stream)), "qlinear_w8a8_i8")
+
+    def qlinear_i8_gemm_i32(self, A, W, Cm, stream=None):
+        M, K = A.shape
+        N = W.shape[0]
+        self.check(self.fn["SNEPPX_qlinear_i8_gemm_i32"](
+            _ptr(A), _ptr(W), _ptr(Cm), M, N, K, self._stream(stream)), "qlinear_i8_gemm_i32")
+
+    def qlinear_w8a8_fp8(self, A, sA, W, sW, out, stream=None):
+        M, K = A.shape
+        N = W.shape[0]
+        self.check(self.fn["SNEPPX_qlinear_w8a8_fp8"](
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), M, N, K, self._stream(stream)), "qlinear_w8a8_fp8")
+
+    # ---------------- HIP events on an explicit stream ----------------------
+    def event(self):
+        e = C.c_void_p()
+        self.check(self.fn["snx_hip_event_create"](C.byref(e)), "event_create")
+        return e
+
+    def record(self, ev, stream=None):
+        self.check(self.fn["snx_hip_event_record"](ev, self._stream(stream)), "event_record")
+
+    def elapsed_ms(self, a, b):
+        self.check(self.fn["snx_hip_event_sync"](b), "event_sync")
+        ms = C.c_float(0)
+        self.check(self.fn["snx_hip_event_elapsed_ms"](C.byref(ms), a, b), "event_elapsed")
+        return ms.value
+
+    def device_info(self):
+        buf = C.create_string_buffer(128)
+        cu, clk = C.c_int(0), C.c_int(0)
+        self.check(self.fn["snx_hip_device_info"](buf, 128, C.byref(cu), C.byref(clk)), "device_info")
+        return buf.value.decode(), cu.value, clk.value
+
+
+_LIB = None
+
+
+def load() -> Library:
+    global _LIB
+    if _LIB is None:
+        _LIB = Library()
+    return _LIB

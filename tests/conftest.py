@@ -31,3 +31,16 @@ def golden():
 def oracle():
     from py_oracle import Oracle
     return Oracle()
+
+
+@pytest.fixture(scope="session")
+def lib():
+    """The product library on a real GPU; a missing GPU or library is a failure."""
+    import torch
+    import sneppx_quant
+    if not torch.cuda.is_available():
+        pytest.fail("gpu test run without a HIP device")
+    lib = sneppx_quant.load()
+    arch, cus, _ = lib.device_info()
+    print(f"[gpu] {arch} with {cus} CUs, library {lib.path}", flush=True)
+    return lib

@@ -1,0 +1,248 @@
+"""Device quantizers and quantized linears (include/sneppx_qlinear.h) on the
+GPU against the CPU oracle.
+
+Bar: codes / packing / scales bit-exact; int32 GEMM accumulators bit-exact;
+fp32-output linears within normwise relative error 1e-4 and bf16-output
+linears within 1e-2 of the fp32 oracle, ||y - y_ref||_inf / ||y_ref||_inf."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL_F32 = 1e-4
+TOL_BF16 = 1e-2
+DEV = "cuda"
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def bf16_bits(x):
+    return torch.from_numpy(np.ascontiguousarray(x, np.float32)).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, np.uint32) << 16).view(np.float32)
+
+
+def u16(t):
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+# ------------------------------------------------------------ quantizers
+@pytest.mark.parametrize("shape", [(1, 1), (5, 333), (4096, 4096), (256, 14336)])
+def test_dev_int8_channel_bit_exact(lib, oracle, shape):
+    print(f"[gpu] int8 channel {shape}", flush=True)
+    rng = np.random.default_rng(sum(shape))
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    w[0, 0] = 0.5 * np.abs(w[0]).max() / 127 * 3          # a tie when scaled
+    q, s = torch.empty(shape, dtype=torch.int8, device=DEV), torch.empty(shape[0], device=DEV)
+    lib.dev_quantize_int8_channel(to_dev(w), q, s)
+    torch.cuda.synchronize()
+    rc, qo, so = oracle.quantize_int8_channel(w)
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("N,K,group", [(24, 512, 128), (11008, 4096, 128), (40, 256, 64), (8, 64, 8)])
+def test_dev_w4_awq_bit_exact(lib, oracle, N, K, group):
+    print(f"[gpu] w4 awq {N}x{K} g{group}", flush=True)
+    rng = np.random.default_rng(N + K)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[1, :group] = 0.125                                   # degenerate group
+    w[2, 0] = np.nan                                       # NaN first element of a group
+    G = K // group
+    qw = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    sc = torch.empty((N, G), dtype=torch.int16, device=DEV)
+    qz = torch.empty((N, (G + 7) // 8), dtype=torch.int32, device=DEV)
+    lib.dev_quantize_w4_awq(to_dev(w), qw, sc, qz, group)
+    torch.cuda.synchronize()
+    rc, qwo, sco, qzo = oracle.w4_awq_quantize(w, group)
+    assert np.array_equal(qw.cpu().numpy().view(np.uint32), qwo)
+    assert np.array_equal(u16(sc), sco)
+    assert np.array_equal(qz.cpu().numpy().view(np.uint32), qzo)
+
+
+@pytest.mark.parametrize("N,K", [(16, 512), (11008, 4096)])
+def test_dev_w4_gptq_actorder_bit_exact(lib, oracle, N, K):
+    print(f"[gpu] w4 gptq act-order {N}x{K}", flush=True)
+    rng = np.random.default_rng(K)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[3, 7] = np.inf                                      # poisons the rest of its group
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    G = K // 128
+    qw = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    sc = torch.empty((N, G), dtype=torch.int16, device=DEV)
+    lib.dev_quantize_w4_gptq(to_dev(w), to_dev(g_idx), G, qw, sc)
+    torch.cuda.synchronize()
+    rc, qwo, sco = oracle.w4_gptq_quantize(w, g_idx, G)
+    assert np.array_equal(qw.cpu().numpy().view(np.uint32), qwo)
+    assert np.array_equal(u16(sc), sco)
+
+
+def test_dev_w4_gptq_rejects_bad_g_idx(lib):
+    w = torch.zeros((2, 16), device=DEV)
+    g = torch.tensor([0] * 15 + [5], dtype=torch.int32, device=DEV)
+    qw = torch.empty((2, 2), dtype=torch.int32, device=DEV)
+    sc = torch.empty((2, 2), dtype=torch.int16, device=DEV)
+    with pytest.raises(Exception, match="g_idx"):
+        lib.dev_quantize_w4_gptq(w, g, 2, qw, sc)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 2048 * 4096])
+def test_dev_fp8_scaled_bit_exact(lib, oracle, n):
+    rng = np.random.default_rng(n)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    out = torch.empty(n, dtype=torch.uint8, device=DEV)
+    s = torch.empty(1, device=DEV)
+    lib.dev_quantize_fp8_e4m3_scaled(to_dev(x), out, s)
+    torch.cuda.synchronize()
+    rc, co, so = oracle.quantize_fp8_e4m3_scaled(x)
+    assert np.array_equal(out.cpu().numpy(), co) and s.item() == so
+
+
+# ---------------------------------------------------------------- linears
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 1000, 4096), (2, 37, 100)])
+def test_w8_gemv(lib, oracle, M, N, K):
+    print(f"[gpu] w8 gemv M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M * N + K)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    rc, q, s = oracle.quantize_int8_channel(w)
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w8_gemv(to_dev(x), to_dev(q), to_dev(s), y)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w8_linear(x, q, s)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
+def _w4_case(oracle, N, K, group, seed, g_idx=None, sym=False):
+    rng = np.random.default_rng(seed)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    if g_idx is not None:
+        G = int(g_idx.max()) + 1
+        rc, qw, sc = oracle.w4_gptq_quantize(w, g_idx, G)
+        return qw, sc, None, G
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, group)
+    if sym:
+        qz = None
+    return qw, sc, qz, K // group
+
+
+@pytest.mark.parametrize("M", [1, 4, 16, 33])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_w4a16_gemv_awq(lib, oracle, M, out):
+    N, K, group = 11008 if M <= 4 else 1376, 4096, 128
+    print(f"[gpu] w4a16 gemv M={M} N={N} out={out}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, M)
+    x = bf16_bits(np.random.default_rng(5 + M).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
+def test_w4a16_gemv_symmetric_and_tails(lib, oracle):
+    # symmetric zero 8 (no qzeros), N not a multiple of 16, K of 1024
+    N, K, group, M = 45, 1024, 256, 3
+    qw, sc, _, G = _w4_case(oracle, N, K, group, 9, sym=True)
+    x = bf16_bits(np.random.default_rng(3).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None, None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, None, None, N, K, group)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_w4a16_gptq_actorder(lib, oracle, M):
+    N, K = 2048, 4096
+    rng = np.random.default_rng(M)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 21, g_idx=g_idx)
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None, to_dev(g_idx), G, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, None, g_idx, N, K, 128)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
+def test_w4a16_odd_group_uses_generic_path(lib, oracle):
+    N, K, group, M = 30, 96, 32, 2
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, 4)
+    x = bf16_bits(np.random.default_rng(4).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 64), (200, 136, 4096), (17, 33, 48)])
+def test_i8_gemm_accumulators_bit_exact(lib, oracle, M, N, K):
+    print(f"[gpu] i8 gemm {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    Cm = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    lib.qlinear_i8_gemm_i32(to_dev(A), to_dev(W), Cm)
+    torch.cuda.synchronize()
+    assert np.array_equal(Cm.cpu().numpy(), oracle.i8_gemm_i32(A, W))
+
+
+def test_w8a8_i8_full_shape_subtiles(lib, oracle):
+    # C4 at full size: accumulators exact on sampled 64x64 sub-tiles, the
+    # bf16 epilogue within 1e-2 of fp32 on dequantised operands.
+    M, N, K = 2048, 14336, 4096
+    print(f"[gpu] w8a8 i8 {M}x{N}x{K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(0)
+    a32 = torch.randn((M, K), device=DEV, generator=g)
+    w32 = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    A = torch.empty((M, K), dtype=torch.int8, device=DEV)
+    W = torch.empty((N, K), dtype=torch.int8, device=DEV)
+    sA, sW = torch.empty(M, device=DEV), torch.empty(N, device=DEV)
+    lib.dev_quantize_int8_channel(a32, A, sA)
+    lib.dev_quantize_int8_channel(w32, W, sW)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w8a8_i8(A, sA, W, sW, out)
+    Cm = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    lib.qlinear_i8_gemm_i32(A, W, Cm)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(1)
+    An, Wn, Cn = A.cpu().numpy(), W.cpu().numpy(), Cm.cpu().numpy()
+    sAn, sWn, outn = sA.cpu().numpy(), sW.cpu().numpy(), bf16_to_f32(u16(out))
+    for _ in range(6):
+        m0, n0 = int(rng.integers(0, M - 64)), int(rng.integers(0, N - 64))
+        ref = oracle.i8_gemm_i32(An[m0:m0 + 64], Wn[n0:n0 + 64])
+        assert np.array_equal(Cn[m0:m0 + 64, n0:n0 + 64], ref)
+        deq = oracle.w8a8_epilogue(ref, sAn[m0:m0 + 64], sWn[n0:n0 + 64])
+        assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], deq) <= TOL_BF16
+    # last rows / columns too
+    ref = oracle.i8_gemm_i32(An[-64:], Wn[-64:])
+    assert np.array_equal(Cn[-64:, -64:], ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 64, 128), (130, 200, 4096)])
+def test_fp8_gemm(lib, oracle, M, N, K):
+    print(f"[gpu] fp8 gemm {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M * N)
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    rc, ca, sa = oracle.quantize_fp8_e4m3_scaled(a)
+    rc, cw, sw = oracle.quantize_fp8_e4m3_scaled(w)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w8a8_fp8(to_dev(ca), to_dev(np.array([sa], np.float32)), to_dev(cw),
+                         to_dev(np.array([sw], np.float32)), out)
+    torch.cuda.synchronize()
+    ref = oracle.fp8_gemm(ca, cw, sa, sw)
+    assert rel_err(bf16_to_f32(u16(out)), ref) <= TOL_BF16
