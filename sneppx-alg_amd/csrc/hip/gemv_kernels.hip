@@ -189,56 +189,204 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__
     }
 }
 
-// Generic W4A16: one wave per output column n, any group layout and M.
-__global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restrict__ x,
-                                                       const uint32_t* __restrict__ qw,
-                                                       const uint16_t* __restrict__ scales,
-                                                       const uint32_t* __restrict__ qz,
-                                                       const int32_t* __restrict__ g_idx,
-                                                       void* __restrict__ y, int y_f32, int M,
-                                                       int N, int K, int G, int group) {
+// Small-M W4A16 (M <= 4): same work split and k-slot order as k_w4a16_gemv,
+// but the activations are staged once per workgroup in LDS, already in the
+// MFMA k-slot order, with their sums X[t][m] over every 128-column step t.
+// Each MFMA then accumulates sum x*(128+q) and the step epilogue subtracts
+// (128+z)*X in fp32, so only one MFMA per packed word is issued.
+// Load order matters because vmcnt retires in issue order: the activation
+// loads go first, then scales/zeros, then the weights, all unconditional
+// (clamped addresses), so staging x never waits for the weight stream.
+// XPT = 16-byte activation items per thread (>= M*K/8/256); MM >= M is the
+// number of output rows the epilogue keeps; the group size is 1 << gshift.
+template <int XPT, int MM, bool ZEROS, bool YF32, bool VS>
+__global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __restrict__ x,
+                                                          const uint32_t* __restrict__ qw,
+                                                          const uint16_t* __restrict__ scales,
+                                                          const uint32_t* __restrict__ qz,
+                                                          void* __restrict__ y, int M, int N,
+                                                          int K, int G, int gshift) {
+    constexpr int CH = 8;
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int xrow = K * 2 + 16;                               // bytes per staged row (+pad)
+    float* xsum = reinterpret_cast<float*>(smem + M * xrow);   // [K/128][4]
+    f32x4* red = reinterpret_cast<f32x4*>(xsum + (K >> 7) * 4);  // [4 waves][64 lanes]
+
     const int lane = threadIdx.x & 63;
-    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (n >= N) return;
-    const int kw = K >> 3, zw = (G + 7) >> 3;
-    for (int m = 0; m < M; m++) {
-        float acc = 0.0f;
-        for (int wd = lane; wd < kw; wd += 64) {
-            const uint32_t w = qw[(size_t)n * kw + wd];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar math
+    const int nl = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int n = n0 + nl < N ? n0 + nl : N - 1;
+    const int k8n = K >> 3, zw = (G + 7) >> 3;
+    const int steps = K >> 9;
+    const int s0 = wave * steps;
+    const uint32_t* wrow = qw + (size_t)n * k8n + kq * 4;
+    const int nitems = M * k8n;
+
+    // 1. activation items (L2-resident after the first workgroups)
+    u32x4 xr[XPT];
 #pragma unroll
-            for (int t = 0; t < 8; t++) {
-                const int k = wd * 8 + t;
-                int g = g_idx ? g_idx[k] : k / group;
-                g = g < 0 ? 0 : (g >= G ? G - 1 : g);   // out-of-range g_idx stays in bounds
-                const int z = qz ? (int)((qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u) : 8;
-                const float deq = (float)((int)((w >> (4 * t)) & 15u) - z) *
-                                  f16_to_f32(scales[(size_t)n * G + g]);
-                acc += bf16_to_f32(x[(size_t)m * K + k]) * deq;
+    for (int i = 0; i < XPT; i++) {
+        int it = threadIdx.x + i * 256;
+        it = it < nitems ? it : nitems - 1;
+        const int m = it / k8n;
+        xr[i] = load16(x + (size_t)m * K + (size_t)(it - m * k8n) * 8);
+    }
+    // keep the activation loads ahead of everything below
+    asm volatile("" ::: "memory");
+    // 2. scales / zeros, 3. weights of the first chunk
+    uint32_t sreg[CH], zreg[CH];
+    u32x4 wv[CH];
+    if (VS) {   // group 128, chunk aligned to 8 groups: one vector load each
+        const u32x4 sv = load16(scales + (size_t)n * G + s0);
+#pragma unroll
+        for (int c = 0; c < CH; c++) sreg[c] = (sv[c >> 1] >> (16 * (c & 1))) & 0xFFFFu;
+        const uint32_t zv = ZEROS ? qz[(size_t)n * zw + (s0 >> 3)] : 0u;
+#pragma unroll
+        for (int c = 0; c < CH; c++) zreg[c] = zv;
+    } else {
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int st = s0 + (c < steps ? c : steps - 1);
+            const int g = (st << 7) >> gshift;
+            sreg[c] = scales[(size_t)n * G + g];
+            zreg[c] = ZEROS ? qz[(size_t)n * zw + (g >> 3)] : 0u;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) wv[c] = load16(wrow + (s0 + (c < steps ? c : steps - 1)) * 16);
+    asm volatile("" ::: "memory");
+
+    // stage x in slot order 0,4,1,5,2,6,3,7 per 8 columns (items past the end
+    // go to a dummy slot so the stores stay unconditional), and sum every 16
+    // consecutive items (one 128-column step) with a 16-lane reduction
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int it = threadIdx.x + i * 256;
+        const bool live = it < nitems;
+        const int m = (live ? it : nitems - 1) / k8n;
+        const int k8 = (live ? it : nitems - 1) - m * k8n;
+        const int off = live ? m * xrow + k8 * 16 : M * xrow - 16;
+        u32x4 p;
+        p[0] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x05040100u);
+        p[1] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x07060302u);
+        p[2] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x05040100u);
+        p[3] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x07060302u);
+        *reinterpret_cast<u32x4*>(smem + off) = p;
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            sum += __builtin_bit_cast(float, xr[i][e] << 16) + __builtin_bit_cast(float, xr[i][e] & 0xFFFF0000u);
+        sum += __shfl_xor(sum, 8);
+        sum += __shfl_xor(sum, 4);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 1);
+        if (live && (k8 & 15) == 0) xsum[(k8 >> 4) * 4 + m] = sum;
+    }
+    __syncthreads();
+
+    // constants for v_and_or_b32: gfx9 VOP3 takes no literals, so they live in registers
+    uint32_t nib_mask, bf_bias;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
+
+    const bool arow = nl < M;
+    const uint8_t* abase = smem + (arow ? nl : 0) * xrow + kq * 64;
+    f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+    for (int sc = 0; sc < steps; sc += CH) {
+        if (sc > 0) {
+#pragma unroll
+            for (int c = 0; c < CH; c++) {
+                const int st = s0 + (sc + c < steps ? sc + c : steps - 1);
+                const int g = (st << 7) >> gshift;
+                sreg[c] = scales[(size_t)n * G + g];
+                zreg[c] = ZEROS ? qz[(size_t)n * zw + (g >> 3)] : 0u;
             }
+#pragma unroll
+            for (int c = 0; c < CH; c++)
+                wv[c] = load16(wrow + (s0 + (sc + c < steps ? sc + c : steps - 1)) * 16);
         }
-        acc = wave_sum(acc);
-        if (lane == 0) {
-            if (y_f32)
-                reinterpret_cast<float*>(y)[(size_t)m * N + n] = acc;
-            else
-                reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(acc);
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            if (sc + c >= steps) break;
+            const int st = s0 + sc + c;
+            const int g = (st << 7) >> gshift;
+            u32x4 a[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) a[j] = u32x4{0u, 0u, 0u, 0u};
+            if (arow) {
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    a[j] = *reinterpret_cast<const u32x4*>(abase + st * 256 + j * 16);
+            }
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t w = wv[c][j];
+                u32x4 b;
+                b[0] = (w & nib_mask) | bf_bias;
+                b[1] = ((w >> 4) & nib_mask) | bf_bias;
+                b[2] = ((w >> 8) & nib_mask) | bf_bias;
+                b[3] = ((w >> 12) & nib_mask) | bf_bias;
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[j]),
+                                                              __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+            }
+            const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)sreg[c]);
+            const uint32_t z = ZEROS ? (zreg[c] >> (4 * (g & 7))) & 15u : 8u;
+            const float corr = sf * (float)(128u + z);
+            const f32x4 xs = *reinterpret_cast<const f32x4*>(xsum + st * 4);
+#pragma unroll
+            for (int i = 0; i < MM; i++) yacc[i] += sf * acc[i] - corr * xs[i];
         }
+    }
+    red[wave * 64 + lane] = yacc;
+    __syncthreads();
+    if (wave != 0 || kq != 0 || n0 + nl >= N) return;
+    const f32x4 v = red[lane] + red[64 + lane] + red[128 + lane] + red[192 + lane];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        if (i >= M) break;
+        if (YF32)
+            reinterpret_cast<float*>(y)[(size_t)i * N + n0 + nl] = v[i];
+        else
+            reinterpret_cast<uint16_t*>(y)[(size_t)i * N + n0 + nl] = f32_to_bf16(v[i]);
     }
 }
 
-template <int MT>
-int launch_w4a16(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
-                 hipStream_t st) {
-    dim3 grid((N + 15) / 16), block(256);
+template <int XPT, int MM, bool VS>
+int launch_small_vs(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                    const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
+                    size_t lds, hipStream_t s) {
+    dim3 grid((unsigned)((N + 15) / 16)), block(256);
+    const int gshift = __builtin_ctz((unsigned)group);
     if (qz) {
-        if (y_f32) k_w4a16_gemv<MT, true, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
-        else k_w4a16_gemv<MT, true, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        if (y_f32) k_w4a16_gemv_small<XPT, MM, true, true, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
+        else k_w4a16_gemv_small<XPT, MM, true, false, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
     } else {
-        if (y_f32) k_w4a16_gemv<MT, false, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
-        else k_w4a16_gemv<MT, false, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        if (y_f32) k_w4a16_gemv_small<XPT, MM, false, true, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
+        else k_w4a16_gemv_small<XPT, MM, false, false, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
     }
-    return snx_launch_check("k_w4a16_gemv");
+    return snx_launch_check("k_w4a16_gemv_small");
+}
+
+template <int XPT, int MM>
+int launch_small_m(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                   const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
+                   size_t lds, hipStream_t s) {
+    // vector scale/zero loads: group 128 and each wave's steps exactly 8
+    const int steps = K >> 9;
+    if (group == 128 && steps == 8 && (G & 7) == 0)
+        return launch_small_vs<XPT, MM, true>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+    return launch_small_vs<XPT, MM, false>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+}
+
+template <int XPT>
+int launch_small(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
+                 size_t lds, hipStream_t s) {
+    if (M == 1) return launch_small_m<XPT, 1>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+    if (M == 2) return launch_small_m<XPT, 2>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+    return launch_small_m<XPT, 4>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
 }
 
 }  // namespace
@@ -266,6 +414,15 @@ int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scal
                      const uint32_t* qzeros, void* y, int y_f32, size_t M, size_t N, size_t K,
                      int group, void* st) {
     const int G = (int)(K / (size_t)group);
+    const size_t lds = M * (K * 2 + 16) + (K / 128) * 16 + 4 * 64 * 16;
+    const size_t items = M * (K / 8);
+    const bool pow2 = (group & (group - 1)) == 0;
+    if (M <= 4 && pow2 && lds <= 65536 && items <= 8 * 256) {
+        const int m = (int)M, n = (int)N, k = (int)K;
+        if (items <= 2 * 256) return launch_small<2>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
+        if (items <= 4 * 256) return launch_small<4>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
+        return launch_small<8>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
+    }
     if (M <= 16)
         return launch_w4a16<1>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
     if (M <= 32)

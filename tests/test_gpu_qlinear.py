@@ -151,6 +151,20 @@ def test_w4a16_gemv_awq(lib, oracle, M, out):
     assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
 
 
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 14336), (2, 64, 2048), (3, 200, 4096)])
+def test_w4a16_gemv_shapes(lib, oracle, M, N, K):
+    # down-projection width, and the small-M kernel's scalar-scale path
+    group = 128
+    print(f"[gpu] w4a16 gemv M={M} N={N} K={K}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, K + M)
+    x = bf16_bits(np.random.default_rng(M).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
 def test_w4a16_gemv_symmetric_and_tails(lib, oracle):
     # symmetric zero 8 (no qzeros), N not a multiple of 16, K of 1024
     N, K, group, M = 45, 1024, 256, 3
