@@ -389,6 +389,58 @@ int launch_small(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
     return launch_small_m<XPT, 4>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
 }
 
+// Generic W4A16: one wave per output column n, any group layout and M.
+__global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restrict__ x,
+                                                       const uint32_t* __restrict__ qw,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint32_t* __restrict__ qz,
+                                                       const int32_t* __restrict__ g_idx,
+                                                       void* __restrict__ y, int y_f32, int M,
+                                                       int N, int K, int G, int group) {
+    const int lane = threadIdx.x & 63;
+    const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (n >= N) return;
+    const int kw = K >> 3, zw = (G + 7) >> 3;
+    for (int m = 0; m < M; m++) {
+        float acc = 0.0f;
+        for (int wd = lane; wd < kw; wd += 64) {
+            const uint32_t w = qw[(size_t)n * kw + wd];
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                const int k = wd * 8 + t;
+                int g = g_idx ? g_idx[k] : k / group;
+                g = g < 0 ? 0 : (g >= G ? G - 1 : g);   // out-of-range g_idx stays in bounds
+                const int z = qz ? (int)((qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u) : 8;
+                const float deq = (float)((int)((w >> (4 * t)) & 15u) - z) *
+                                  f16_to_f32(scales[(size_t)n * G + g]);
+                acc += bf16_to_f32(x[(size_t)m * K + k]) * deq;
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) {
+            if (y_f32)
+                reinterpret_cast<float*>(y)[(size_t)m * N + n] = acc;
+            else
+                reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(acc);
+        }
+    }
+}
+
+template <int MT>
+int launch_w4a16(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
+                 hipStream_t st) {
+    dim3 grid((N + 15) / 16), block(256);
+    if (qz) {
+        if (y_f32) k_w4a16_gemv<MT, true, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        else k_w4a16_gemv<MT, true, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+    } else {
+        if (y_f32) k_w4a16_gemv<MT, false, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        else k_w4a16_gemv<MT, false, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+    }
+    return snx_launch_check("k_w4a16_gemv");
+}
+
 }  // namespace
 
 extern "C" {
