@@ -125,17 +125,26 @@ __global__ void __launch_bounds__(256) k_fp8_gemm(const uint8_t* __restrict__ A,
 
 // ------------------------------------------------------------ tiled GEMM
 // Workgroup tile 256 (M) x 224 (N); 4 waves in 2 x 2, each 128 x 112 =
-// 8 x 7 MFMA blocks of 16 x 16.  K advances in 128-byte stages staged in LDS
-// (row stride 144 B: 16 rows of one fragment read land on distinct banks),
-// double-buffered: global loads for stage t+1 are issued before the MFMAs of
-// stage t and written to the other buffer after them, one barrier per stage.
-// int8 uses two v_mfma_i32_16x16x64_i8 k-halves per stage, fp8 one
-// v_mfma_f32_16x16x128_f8f6f4.  Tiles are mapped so that each XCD (the
-// dispatcher deals workgroups to the 8 XCDs round-robin) owns a compact
-// 8 x (tiles_n / 8) block and keeps its A and W rows in its own L2.
-constexpr int TBM = 256, TBN = 224, TBK = 128, TLDS = 144;
-constexpr int TFM = 8, TFN = 7;   // fragments per wave
-constexpr int TLDS_A = TBM * TLDS, TLDS_B = TBN * TLDS, TLDS_STAGE = TLDS_A + TLDS_B;
+// 8 x 7 MFMA blocks of 16 x 16.  K advances in 128-byte stages, double
+// buffered in LDS (2 x 60 KB).  Operands go global -> LDS directly
+// (global_load_lds_dwordx4: no staging registers, no ds_write): each wave
+// instruction fills 8 rows x 128 B.  16-byte chunk c of tile row R sits at
+// slot c ^ swz(R), swz(R) = (R & 7) ^ ((R >> 3) & 1): it depends on R mod 16
+// only (fragment rows share it), and the 16 rows of a fragment read hit
+// distinct bank groups whether LDS serves 8 or 16 lanes a cycle.
+// Per stage: loads for stage t+1 issued first; k-half 0 MFMAs (next half's
+// fragments in flight); wait for the loads + barrier; k-half 1 MFMAs while
+// stage t+1's first fragments are read.  int8: v_mfma_i32_16x16x64_i8 per
+// k-half; fp8: the stage's one v_mfma_f32_16x16x128_f8f6f4 k-step split by
+// fragment rows 0-3 / 4-7.  Tiles are dealt so each XCD (workgroups go to
+// the 8 XCDs round-robin) owns a compact 8 x (tiles_n / 8) block.
+constexpr int TBM = 256, TBN = 224, TBK = 128;
+constexpr int TFM = 8, TFN = 7;                          // fragments per wave
+constexpr int TLDS_A = TBM * TBK, TLDS_B = TBN * TBK, TLDS_STAGE = TLDS_A + TLDS_B;
+
+__device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+__device__ __forceinline__ i32x4 lds16(const int8_t* p) { return *reinterpret_cast<const i32x4*>(p); }
 
 template <bool FP8, bool RAW>
 __global__ void __launch_bounds__(256) k_gemm_tiled(const int8_t* __restrict__ A,
@@ -151,48 +160,35 @@ __global__ void __launch_bounds__(256) k_gemm_tiled(const int8_t* __restrict__ A
     const int wm = wave >> 1, wn = wave & 1;
     const int r16 = lane & 15, q = lane >> 4;
 
-    // XCD-aware tile order
     const int b = blockIdx.x, nb = gridDim.x;
-    int tile;
-    if (nb % 8 == 0) {
-        const int per = nb / 8;
-        tile = (b % 8) * per + b / 8;
-    } else {
-        tile = b;
-    }
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
     const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int m0 = tm * TBM, n0 = tn * TBN;
 
-    // global -> LDS staging: A 2048 chunks (8/thread), W 1792 chunks (7/thread);
-    // thread t moves chunk (row t/8 + 32 i, 16-byte column t%8).  Global
-    // offsets are 32-bit (the launcher checks M*K and N*K fit).
-    const int srow = tid >> 3, scol = (tid & 7) * 16;
+    // direct-load sources: wave w, instruction i fills tile rows
+    // 8*(4 i + w) .. +8; lane s takes row +s/8, slot s%8 <- chunk slot^swz(row)
+    const int lrow = lane >> 3, lslot = lane & 7;
     uint32_t ga[8], gw[7];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int gr = m0 + srow + 32 * i < M ? m0 + srow + 32 * i : M - 1;
-        ga[i] = (uint32_t)gr * (uint32_t)K + scol;
+        const int row = (4 * i + wave) * 8 + lrow;
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
     }
 #pragma unroll
     for (int i = 0; i < 7; i++) {
-        const int gr = n0 + srow + 32 * i < N ? n0 + srow + 32 * i : N - 1;
-        gw[i] = (uint32_t)gr * (uint32_t)K + scol;
+        const int row = (4 * i + wave) * 8 + lrow;
+        const int gr = n0 + row < N ? n0 + row : N - 1;
+        gw[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
     }
-    const int lbase = srow * TLDS + scol;
-
-    i32x4 ra[8], rw[7];
-    auto gload = [&](int k0) {
+    auto dload = [&](int buf, int k0) {
+        int8_t* base = lds + buf * TLDS_STAGE;
 #pragma unroll
-        for (int i = 0; i < 8; i++) ra[i] = *reinterpret_cast<const i32x4*>(A + ga[i] + k0);
+        for (int i = 0; i < 8; i++)
+            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (4 * i + wave) * 1024, 16, 0, 0);
 #pragma unroll
-        for (int i = 0; i < 7; i++) rw[i] = *reinterpret_cast<const i32x4*>(W + gw[i] + k0);
-    };
-    auto lstore = [&](int buf) {
-        int8_t* base = lds + buf * TLDS_STAGE + lbase;
-#pragma unroll
-        for (int i = 0; i < 8; i++) *reinterpret_cast<i32x4*>(base + i * 32 * TLDS) = ra[i];
-#pragma unroll
-        for (int i = 0; i < 7; i++) *reinterpret_cast<i32x4*>(base + TLDS_A + i * 32 * TLDS) = rw[i];
+        for (int i = 0; i < 7; i++)
+            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (4 * i + wave) * 1024, 16, 0, 0);
     };
 
     typedef typename std::conditional<FP8, f32x4, i32x4>::type acc_t;
@@ -202,81 +198,122 @@ __global__ void __launch_bounds__(256) k_gemm_tiled(const int8_t* __restrict__ A
 #pragma unroll
         for (int j = 0; j < TFN; j++) acc[i][j] = acc_t{0, 0, 0, 0};
 
-    const int a_off = (wm * 128 + r16) * TLDS;
-    const int w_off = TLDS_A + (wn * 112 + r16) * TLDS;
+    // fragment rows: R = wm*128 + i*16 + r16 (A), wn*112 + j*16 + r16 (W);
+    // swz(R) depends on r16 only, so the byte offset of chunk c is fixed per lane
+    const int sw = swz(r16);
+    const int8_t* arow = lds + (wm * 128 + r16) * TBK;
+    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
     const int nk = K / TBK;
 
-    gload(0);
-    lstore(0);
+    dload(0, 0);
+    __builtin_amdgcn_s_waitcnt(0x0070);      // vmcnt(0) lgkmcnt(0): stage 0 landed in LDS
     __syncthreads();
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * TBK);
-        const int8_t* base = lds + cur * TLDS_STAGE;
-        if (FP8) {
-            i32x8 fa[TFM], fw[TFN];
+
+    if (!FP8) {
+        i32x4 fa[2][TFM], fw[2][TFN];
+        // fragments of stage 0, k-half 0: chunk q
 #pragma unroll
-            for (int i = 0; i < TFM; i++) {
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(base + a_off + i * 16 * TLDS + q * 32);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(base + a_off + i * 16 * TLDS + q * 32 + 16);
-                fa[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            }
+        for (int i = 0; i < TFM; i++) fa[0][i] = lds16(arow + i * 16 * TBK + ((q ^ sw) << 4));
 #pragma unroll
-            for (int j = 0; j < TFN; j++) {
-                const i32x4 lo = *reinterpret_cast<const i32x4*>(base + w_off + j * 16 * TLDS + q * 32);
-                const i32x4 hi = *reinterpret_cast<const i32x4*>(base + w_off + j * 16 * TLDS + q * 32 + 16);
-                fw[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        for (int j = 0; j < TFN; j++) fw[0][j] = lds16(wrow + j * 16 * TBK + ((q ^ sw) << 4));
+        for (int kt = 0; kt < nk; kt++) {
+            const int cur = kt & 1;
+            const int8_t* ab = arow + cur * TLDS_STAGE;
+            const int8_t* wb = wrow + cur * TLDS_STAGE;
+            // loads for stage t+1 (the last stage re-reads stage 0: in
+            // bounds, never used) keep the loop body branch-free
+            dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
+            // k-half 1 fragments (chunk 4 + q) while k-half 0 computes
+#pragma unroll
+            for (int i = 0; i < TFM; i++) fa[1][i] = lds16(ab + i * 16 * TBK + (((4 + q) ^ sw) << 4));
+#pragma unroll
+            for (int j = 0; j < TFN; j++) fw[1][j] = lds16(wb + j * 16 * TBK + (((4 + q) ^ sw) << 4));
+#pragma unroll
+            for (int i = 0; i < TFM; i++)
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[0][i], fw[0][j], (i32x4)acc[i][j], 0, 0, 0);
+            // stage t+1 landed (vmcnt) and this wave's reads of stage t are
+            // done (lgkmcnt) before any wave may overwrite stage t's buffer
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0070);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                const int8_t* an = arow + (cur ^ 1) * TLDS_STAGE;
+                const int8_t* wnx = wrow + (cur ^ 1) * TLDS_STAGE;
+#pragma unroll
+                for (int i = 0; i < TFM; i++) fa[0][i] = lds16(an + i * 16 * TBK + ((q ^ sw) << 4));
+#pragma unroll
+                for (int j = 0; j < TFN; j++) fw[0][j] = lds16(wnx + j * 16 * TBK + ((q ^ sw) << 4));
             }
 #pragma unroll
             for (int i = 0; i < TFM; i++)
 #pragma unroll
                 for (int j = 0; j < TFN; j++)
-                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        fa[i], fw[j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
-        } else {
+                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[1][i], fw[1][j], (i32x4)acc[i][j], 0, 0, 0);
+        }
+    } else {
+        // fp8: per lane 32 bytes = chunks 2q, 2q+1
+        auto rd32 = [&](const int8_t* rowp) {
+            const i32x4 lo = lds16(rowp + (((2 * q) ^ sw) << 4));
+            const i32x4 hi = lds16(rowp + (((2 * q + 1) ^ sw) << 4));
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        i32x8 fw[2][TFN], fa[TFM];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                i32x4 fa[TFM], fw[TFN];
+        for (int j = 0; j < TFN; j++) fw[0][j] = rd32(wrow + j * 16 * TBK);
 #pragma unroll
-                for (int i = 0; i < TFM; i++)
-                    fa[i] = *reinterpret_cast<const i32x4*>(base + a_off + i * 16 * TLDS + h * 64 + q * 16);
+        for (int i = 0; i < 4; i++) fa[i] = rd32(arow + i * 16 * TBK);
+        for (int kt = 0; kt < nk; kt++) {
+            const int cur = kt & 1;
+            const int8_t* ab = arow + cur * TLDS_STAGE;
+            dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
+#pragma unroll
+            for (int i = 4; i < 8; i++) fa[i] = rd32(ab + i * 16 * TBK);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
 #pragma unroll
                 for (int j = 0; j < TFN; j++)
-                    fw[j] = *reinterpret_cast<const i32x4*>(base + w_off + j * 16 * TLDS + h * 64 + q * 16);
+                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        fa[i], fw[0][j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0070);
+            __syncthreads();
+            __builtin_amdgcn_sched_barrier(0);
+            {
+                const int8_t* an = arow + (cur ^ 1) * TLDS_STAGE;
+                const int8_t* wnx = wrow + (cur ^ 1) * TLDS_STAGE;
 #pragma unroll
-                for (int i = 0; i < TFM; i++)
+                for (int j = 0; j < TFN; j++) fw[1][j] = rd32(wnx + j * 16 * TBK);
 #pragma unroll
-                    for (int j = 0; j < TFN; j++)
-                        acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fw[j], (i32x4)acc[i][j], 0, 0, 0);
+                for (int i = 0; i < 4; i++) fa[i] = rd32(an + i * 16 * TBK);
             }
+#pragma unroll
+            for (int i = 4; i < 8; i++)
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        fa[i], fw[0][j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < TFN; j++) fw[0][j] = fw[1][j];
         }
-        if (kt + 1 < nk) lstore(cur ^ 1);
-        __syncthreads();
     }
 
     // epilogue: C row 4*(lane/16)+e, col lane%16 of each 16 x 16 block
-    float sa_tile[TFM][4];
-    float sw_tile[TFN];
-    if (!RAW) {
 #pragma unroll
-        for (int i = 0; i < TFM; i++)
+    for (int i = 0; i < TFM; i++) {
+        float sa[4];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 128 + i * 16 + q * 4 + e;
-                sa_tile[i][e] = FP8 ? sA[0] : sA[m < M ? m : M - 1];
-            }
-#pragma unroll
-        for (int j = 0; j < TFN; j++) {
-            const int n = n0 + wn * 112 + j * 16 + r16;
-            sw_tile[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + wm * 128 + i * 16 + q * 4 + e;
+            sa[e] = RAW ? 0.0f : (FP8 ? sA[0] : sA[m < M ? m : M - 1]);
         }
-    }
-#pragma unroll
-    for (int i = 0; i < TFM; i++)
 #pragma unroll
         for (int j = 0; j < TFN; j++) {
             const int n = n0 + wn * 112 + j * 16 + r16;
             if (n >= N) continue;
+            const float swv = RAW ? 0.0f : (FP8 ? sW[0] : sW[n]);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = m0 + wm * 128 + i * 16 + q * 4 + e;
@@ -284,9 +321,143 @@ __global__ void __launch_bounds__(256) k_gemm_tiled(const int8_t* __restrict__ A
                 if (RAW)
                     Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
                 else
-                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sa_tile[i][e] * sw_tile[j]);
+                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sa[e] * swv);
             }
         }
+    }
+}
+
+// Eight-wave variant of the same tile: waves in 4 (M) x 2 (N), each 64 x 112
+// = 4 x 7 MFMA blocks (112 accumulators), two waves per SIMD, so one wave's
+// LDS latency hides behind the other's MFMAs without intra-wave prefetch.
+// Same LDS layout, swizzle, direct loads and XCD tile order as above.
+template <bool FP8, bool RAW>
+__global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
+                                                 const int8_t* __restrict__ W,
+                                                 const float* __restrict__ sA,
+                                                 const float* __restrict__ sW,
+                                                 int32_t* __restrict__ Craw,
+                                                 uint16_t* __restrict__ out, int M, int N, int K,
+                                                 int tiles_m, int tiles_n) {
+    constexpr int FM = 4;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, q = lane >> 4;
+
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * TBM, n0 = tn * TBN;
+
+    // direct loads: A block 8*w' + ... : wave w, instruction i fills 1 KB block
+    // i*8 + w (8 tile rows); A has 32 blocks, W 28
+    const int lrow = lane >> 3, lslot = lane & 7;
+    uint32_t ga[4], gw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (8 * i + wave) * 8 + lrow;
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
+        const int wr = row < TBN ? row : TBN - 1;
+        const int gn = n0 + wr < N ? n0 + wr : N - 1;
+        gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
+    }
+    auto dload = [&](int buf, int k0) {
+        int8_t* base = lds + buf * TLDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
+        if (wave < 4)
+            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
+    };
+
+    typedef typename std::conditional<FP8, f32x4, i32x4>::type acc_t;
+    acc_t acc[FM][TFN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < TFN; j++) acc[i][j] = acc_t{0, 0, 0, 0};
+
+    const int sw = swz(r16);
+    const int8_t* arow = lds + (wm * 64 + r16) * TBK;
+    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
+    const int nk = K / TBK;
+
+    dload(0, 0);
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
+        __syncthreads();
+        // loads for stage t+1 into the other buffer (last stage: stage 0 again, unused)
+        dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
+        const int8_t* ab = arow + cur * TLDS_STAGE;
+        const int8_t* wb = wrow + cur * TLDS_STAGE;
+        if (!FP8) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                i32x4 fa[FM], fw[TFN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) fa[i] = lds16(ab + i * 16 * TBK + (((4 * h + q) ^ sw) << 4));
+#pragma unroll
+                for (int j = 0; j < TFN; j++) fw[j] = lds16(wb + j * 16 * TBK + (((4 * h + q) ^ sw) << 4));
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < TFN; j++)
+                        acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fw[j], (i32x4)acc[i][j], 0, 0, 0);
+            }
+        } else {
+            i32x8 fa[FM], fw[TFN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const i32x4 lo = lds16(ab + i * 16 * TBK + (((2 * q) ^ sw) << 4));
+                const i32x4 hi = lds16(ab + i * 16 * TBK + (((2 * q + 1) ^ sw) << 4));
+                fa[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int j = 0; j < TFN; j++) {
+                const i32x4 lo = lds16(wb + j * 16 * TBK + (((2 * q) ^ sw) << 4));
+                const i32x4 hi = lds16(wb + j * 16 * TBK + (((2 * q + 1) ^ sw) << 4));
+                fw[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        fa[i], fw[j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        float sa[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+            sa[e] = RAW ? 0.0f : (FP8 ? sA[0] : sA[m < M ? m : M - 1]);
+        }
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            const int n = n0 + wn * 112 + j * 16 + r16;
+            if (n >= N) continue;
+            const float swv = RAW ? 0.0f : (FP8 ? sW[0] : sW[n]);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+                if (m >= M) continue;
+                if (RAW)
+                    Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
+                else
+                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sa[e] * swv);
+            }
+        }
+    }
 }
 
 template <bool FP8, bool RAW>
@@ -300,16 +471,16 @@ int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float*
     const size_t lds = 2 * (size_t)TLDS_STAGE;
     static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_tiled<FP8, RAW>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_8w<FP8, RAW>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
             return -1;
         }
         attr_set = true;
     }
-    k_gemm_tiled<FP8, RAW><<<tiles_m * tiles_n, 256, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
-                                                               tiles_m, tiles_n);
-    return snx_launch_check("k_gemm_tiled");
+    k_gemm_8w<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
+                                                            tiles_m, tiles_n);
+    return snx_launch_check("k_gemm_8w");
 }
 
 }  // namespace
