@@ -40,6 +40,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "copy"],
+                   help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
 
@@ -204,6 +206,41 @@ def cpu_baseline(ws_host, x_host, N, K, group, seconds):
             "host_cpu": _cpu_name(), "host_threads_available": os.cpu_count()}
 
 
+def load_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` from profiles/traffic.json (written
+    from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE passes, calibrated on a copy
+    of known size); None when absent."""
+    path = os.path.join(REPO, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+    if not rec:
+        return None
+    return int(rec["fetch_bytes"] + rec["write_bytes"])
+
+
+def run_only(args, lib, timer, torch, N, K, group):
+    """One kernel family, for profiler passes (prints one line, no JSON)."""
+    steps = args.steps
+    if args.only == "gemv":
+        r, _ = bench_w4a16(lib, timer, torch, 1, N, K, group, args.copies, steps, args.warmup)
+        print(f"gemv C2 M=1: {r['ms_per_step'] * 1e3:.3f} us/launch, {r['gbs']:.0f} GB/s")
+    elif args.only in ("gemm-i8", "gemm-fp8"):
+        r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, steps, 2, fp8=args.only == "gemm-fp8")
+        print(f"{args.only}: {r['ms_per_step'] * 1e3:.1f} us/launch, {r['tops']:.0f} TOPS")
+    else:
+        # a plain device copy of known size, the calibration for FETCH/WRITE_SIZE
+        n = 256 << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copy: {steps} x {n} bytes")
+
+
 def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -231,6 +268,9 @@ def main():
     timer = Timer(lib, stream)
 
     N, K, group, M = 11008, 4096, 128, 1
+    if args.only:
+        run_only(args, lib, timer, torch, N, K, group)
+        return
     head, keep = bench_w4a16(lib, timer, torch, M, N, K, group, args.copies, args.steps, args.warmup)
     print(f"[bench] C2 M=1: {head['gbs']:.0f} GB/s whole-job, kernel {head['launch_ms_mean'] * 1e3:.2f} us",
           file=sys.stderr, flush=True)
@@ -269,7 +309,10 @@ def main():
         xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
         cpu = cpu_baseline(host, xh, N, K, group, args.cpu_seconds)
 
-    achieved = head["bytes"] / head["launch_ms_mean"] / 1e6
+    # per-launch duration = back-to-back time / launches (>= kernel time; it
+    # matches rocprofv3's kernel-trace average to within the launch gap)
+    achieved = head["bytes"] / head["ms_per_step"] / 1e6
+    traffic = load_traffic("k_w4a16_gemv_small")
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),
@@ -287,9 +330,10 @@ def main():
                    "group": group, "weight_copies": args.copies,
                    "bytes_per_step": head["bytes"], "device": arch, "cus": cus},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_w4a16_gemv", "launch_us_mean": round(head["launch_ms_mean"] * 1e3, 3),
-                     "launch_us_median": round(head["launch_ms_median"] * 1e3, 3)},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "k_w4a16_gemv_small", "algorithmic_bytes": head["bytes"],
+                     "launch_us": round(head["ms_per_step"] * 1e3, 3),
+                     "event_pair_us_median": round(head["launch_ms_median"] * 1e3, 3)},
         "cpu_baseline": cpu,
         "extra": extra,
     }

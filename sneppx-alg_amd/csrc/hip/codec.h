@@ -110,4 +110,11 @@ SNX_HD uint16_t f32_to_bf16(float f) {
 
 SNX_HD float bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
 
+// Output conversion of the linear kernels: gfx950's v_cvt_pk_bf16_f32 (round
+// to nearest even, NaN stays NaN) -- the same value as f32_to_bf16 for every
+// non-NaN input.
+__device__ __forceinline__ uint16_t bf16_out(float f) {
+    return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
 }  // namespace snx

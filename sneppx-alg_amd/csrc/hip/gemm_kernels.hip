@@ -389,6 +389,22 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
     const int nk = K / TBK;
 
     dload(0, 0);
+    // epilogue scales, fetched now so their latency hides under the K loop
+    float sa[FM][4], swv[TFN];
+    if (!RAW) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+                sa[i][e] = FP8 ? sA[0] : sA[m < M ? m : M - 1];
+            }
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            const int n = n0 + wn * 112 + j * 16 + r16;
+            swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
+        }
+    }
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
         __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
@@ -401,10 +417,13 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 i32x4 fa[FM], fw[TFN];
+                // k-half h takes chunks 2q + h (the even / odd chunks, the
+                // same bank pattern as the fp8 reads; any k order works as
+                // long as A and W agree)
 #pragma unroll
-                for (int i = 0; i < FM; i++) fa[i] = lds16(ab + i * 16 * TBK + (((4 * h + q) ^ sw) << 4));
+                for (int i = 0; i < FM; i++) fa[i] = lds16(ab + i * 16 * TBK + (((2 * q + h) ^ sw) << 4));
 #pragma unroll
-                for (int j = 0; j < TFN; j++) fw[j] = lds16(wb + j * 16 * TBK + (((4 * h + q) ^ sw) << 4));
+                for (int j = 0; j < TFN; j++) fw[j] = lds16(wb + j * 16 * TBK + (((2 * q + h) ^ sw) << 4));
 #pragma unroll
                 for (int i = 0; i < FM; i++)
 #pragma unroll
@@ -436,17 +455,10 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
 
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        float sa[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
-            sa[e] = RAW ? 0.0f : (FP8 ? sA[0] : sA[m < M ? m : M - 1]);
-        }
 #pragma unroll
         for (int j = 0; j < TFN; j++) {
             const int n = n0 + wn * 112 + j * 16 + r16;
             if (n >= N) continue;
-            const float swv = RAW ? 0.0f : (FP8 ? sW[0] : sW[n]);
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
@@ -454,7 +466,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                 if (RAW)
                     Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
                 else
-                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sa[e] * swv);
+                    out[(size_t)m * N + n] = bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j]);
             }
         }
     }
