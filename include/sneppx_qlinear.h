@@ -85,6 +85,26 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
                          void* y, SNEPPXDtype y_dtype, size_t M, size_t N, size_t K,
                          int group, SNEPPXStream stream);
 
+/* C3 fast path, step 1 (once per layer, at load time): GPTQ act-order
+ * weights (qweight in column order k, g_idx int32 [K]) -> group-contiguous
+ * order.  perm (uint16 [K], device) receives the stable argsort of g_idx and
+ * qweight_sorted[n] holds column perm[k'] of row n at position k'.  Every
+ * group must hold exactly K/G columns (g_idx = order // group, as GPTQ writes
+ * it); otherwise -1 and the caller keeps SNEPPX_qlinear_w4a16 with g_idx.
+ * K <= 65536.  Synchronous (g_idx is sorted on the host). */
+int SNEPPX_qlinear_w4_actorder_prepare(const uint32_t* qweight, const int32_t* g_idx, size_t G,
+                                       uint32_t* qweight_sorted, uint16_t* perm,
+                                       size_t N, size_t K, SNEPPXStream stream);
+
+/* C3 fast path, step 2: y = x . W^T for prepared weights.  Scales (and
+ * optional qzeros) stay [N][G] in group order; the group of sorted column k'
+ * is k' / group with group = K/G.  The activations are gathered by perm
+ * inside the decode kernel (M <= 4) or by one gather pass (other M). */
+int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sorted,
+                                  const uint16_t* scales, const uint32_t* qzeros,
+                                  const uint16_t* perm, void* y, SNEPPXDtype y_dtype,
+                                  size_t M, size_t N, size_t K, int group, SNEPPXStream stream);
+
 /* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n]), acc = sum_k A*W in
  * int32 (exact).  A int8 [M][K] (per-token scales sA fp32 [M]), W int8 [N][K]
  * (per-channel sW fp32 [N]), out bf16 [M][N]. */

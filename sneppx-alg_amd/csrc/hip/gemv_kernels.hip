@@ -199,11 +199,17 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__
 // (clamped addresses), so staging x never waits for the weight stream.
 // XPT = 16-byte activation items per thread (>= M*K/8/256); MM >= M is the
 // number of output rows the epilogue keeps; the group size is 1 << gshift.
-template <int XPT, int MM, bool ZEROS, bool YF32, bool VS>
+// PERM: the weight columns are stored in the order perm (uint16 [K]; column
+// k' of qw is column perm[k'] of the layer), so the activations are gathered
+// the same way: raw x and perm go to LDS first, then each item is rebuilt
+// from LDS as x[m][perm[k']] before the slot-order staging.  No global load
+// depends on another, so the weight stream is issued exactly as without it.
+template <int XPT, int MM, bool ZEROS, bool YF32, bool VS, bool PERM>
 __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __restrict__ x,
                                                           const uint32_t* __restrict__ qw,
                                                           const uint16_t* __restrict__ scales,
                                                           const uint32_t* __restrict__ qz,
+                                                          const uint16_t* __restrict__ perm,
                                                           void* __restrict__ y, int M, int N,
                                                           int K, int G, int gshift) {
     constexpr int CH = 8;
@@ -211,6 +217,8 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     const int xrow = K * 2 + 16;                               // bytes per staged row (+pad)
     float* xsum = reinterpret_cast<float*>(smem + M * xrow);   // [K/128][4]
     f32x4* red = reinterpret_cast<f32x4*>(xsum + (K >> 7) * 4);  // [4 waves][64 lanes]
+    uint16_t* xraw = reinterpret_cast<uint16_t*>(red + 256);   // PERM: [M][K] source order
+    uint16_t* pl = xraw + M * K;                               // PERM: [K]
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar math
@@ -231,6 +239,15 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
         it = it < nitems ? it : nitems - 1;
         const int m = it / k8n;
         xr[i] = load16(x + (size_t)m * K + (size_t)(it - m * k8n) * 8);
+    }
+    u32x4 pr[PERM ? XPT : 1];
+    if (PERM) {   // perm items: K/8 <= nitems, same item grid
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            int it = threadIdx.x + i * 256;
+            it = it < k8n ? it : k8n - 1;
+            pr[i] = load16(perm + (size_t)it * 8);
+        }
     }
     // keep the activation loads ahead of everything below
     asm volatile("" ::: "memory");
@@ -256,6 +273,37 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
 #pragma unroll
     for (int c = 0; c < CH; c++) wv[c] = load16(wrow + (s0 + (c < steps ? c : steps - 1)) * 16);
     asm volatile("" ::: "memory");
+
+    if (PERM) {
+        // raw activations and perm to LDS (clamped items rewrite the last
+        // item with its own value), then gather each item in perm order
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            int it = threadIdx.x + i * 256;
+            it = it < nitems ? it : nitems - 1;
+            *reinterpret_cast<u32x4*>(xraw + (size_t)it * 8) = xr[i];
+            int ip = threadIdx.x + i * 256;
+            ip = ip < k8n ? ip : k8n - 1;
+            *reinterpret_cast<u32x4*>(pl + (size_t)ip * 8) = pr[i];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            int it = threadIdx.x + i * 256;
+            it = it < nitems ? it : nitems - 1;
+            const int m = it / k8n;
+            const int k8 = it - m * k8n;
+            const u32x4 pv = *reinterpret_cast<const u32x4*>(pl + k8 * 8);
+            const uint16_t* xm = xraw + m * K;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t lo = pv[e] & 0xFFFFu, hi = pv[e] >> 16;
+                lo = lo < (uint32_t)K ? lo : (uint32_t)K - 1u;   // caller's perm stays in LDS bounds
+                hi = hi < (uint32_t)K ? hi : (uint32_t)K - 1u;
+                xr[i][e] = (uint32_t)xm[lo] | (uint32_t)xm[hi] << 16;
+            }
+        }
+    }
 
     // stage x in slot order 0,4,1,5,2,6,3,7 per 8 columns (items past the end
     // go to a dummy slot so the stores stay unconditional), and sum every 16
@@ -353,40 +401,49 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     }
 }
 
-template <int XPT, int MM, bool VS>
-int launch_small_vs(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                    const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
-                    size_t lds, hipStream_t s) {
-    dim3 grid((unsigned)((N + 15) / 16)), block(256);
-    const int gshift = __builtin_ctz((unsigned)group);
-    if (qz) {
-        if (y_f32) k_w4a16_gemv_small<XPT, MM, true, true, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
-        else k_w4a16_gemv_small<XPT, MM, true, false, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
+struct W4Launch {
+    const uint16_t* x;
+    const uint32_t* qw;
+    const uint16_t* scales;
+    const uint32_t* qz;
+    const uint16_t* perm;
+    void* y;
+    int y_f32, M, N, K, G, group;
+    size_t lds;
+    hipStream_t s;
+};
+
+template <int XPT, int MM, bool VS, bool PERM>
+int launch_small_vs(const W4Launch& a) {
+    dim3 grid((unsigned)((a.N + 15) / 16)), block(256);
+    const int gshift = __builtin_ctz((unsigned)a.group);
+#define SNX_SMALL(Z, F)                                                                         \
+    k_w4a16_gemv_small<XPT, MM, Z, F, VS, PERM><<<grid, block, a.lds, a.s>>>(                   \
+        a.x, a.qw, a.scales, a.qz, a.perm, a.y, a.M, a.N, a.K, a.G, gshift)
+    if (a.qz) {
+        if (a.y_f32) SNX_SMALL(true, true);
+        else SNX_SMALL(true, false);
     } else {
-        if (y_f32) k_w4a16_gemv_small<XPT, MM, false, true, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
-        else k_w4a16_gemv_small<XPT, MM, false, false, VS><<<grid, block, lds, s>>>(x, qw, scales, qz, y, M, N, K, G, gshift);
+        if (a.y_f32) SNX_SMALL(false, true);
+        else SNX_SMALL(false, false);
     }
+#undef SNX_SMALL
     return snx_launch_check("k_w4a16_gemv_small");
 }
 
-template <int XPT, int MM>
-int launch_small_m(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                   const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
-                   size_t lds, hipStream_t s) {
+template <int XPT, int MM, bool PERM>
+int launch_small_m(const W4Launch& a) {
     // vector scale/zero loads: group 128 and each wave's steps exactly 8
-    const int steps = K >> 9;
-    if (group == 128 && steps == 8 && (G & 7) == 0)
-        return launch_small_vs<XPT, MM, true>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
-    return launch_small_vs<XPT, MM, false>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+    const int steps = a.K >> 9;
+    if (a.group == 128 && steps == 8 && (a.G & 7) == 0) return launch_small_vs<XPT, MM, true, PERM>(a);
+    return launch_small_vs<XPT, MM, false, PERM>(a);
 }
 
-template <int XPT>
-int launch_small(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
-                 size_t lds, hipStream_t s) {
-    if (M == 1) return launch_small_m<XPT, 1>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
-    if (M == 2) return launch_small_m<XPT, 2>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
-    return launch_small_m<XPT, 4>(x, qw, scales, qz, y, y_f32, M, N, K, G, group, lds, s);
+template <int XPT, bool PERM>
+int launch_small(const W4Launch& a) {
+    if (a.M == 1) return launch_small_m<XPT, 1, PERM>(a);
+    if (a.M == 2) return launch_small_m<XPT, 2, PERM>(a);
+    return launch_small_m<XPT, 4, PERM>(a);
 }
 
 // Generic W4A16: one wave per output column n, any group layout and M.
@@ -441,9 +498,57 @@ int launch_w4a16(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
     return snx_launch_check("k_w4a16_gemv");
 }
 
+// Column gather of the activations: xs[m][k'] = x[m][perm[k']].
+__global__ void __launch_bounds__(256) k_gather_cols(const uint16_t* __restrict__ x,
+                                                     const uint16_t* __restrict__ perm,
+                                                     uint16_t* __restrict__ xs, int K, size_t total) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const size_t m = i / (size_t)K;
+    const int k = (int)(i - m * (size_t)K);
+    int src = perm[k];
+    src = src < K ? src : K - 1;
+    xs[i] = x[m * K + src];
+}
+
+// Packed uint4 column permutation: one output word (8 columns) per thread.
+__global__ void __launch_bounds__(256) k_w4_permute_cols(const uint32_t* __restrict__ qw,
+                                                         const uint16_t* __restrict__ perm,
+                                                         uint32_t* __restrict__ qs, int K,
+                                                         size_t words) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= words) return;
+    const int k8n = K >> 3;
+    const size_t n = i / (size_t)k8n;
+    const int w = (int)(i - n * (size_t)k8n);
+    const uint32_t* row = qw + n * (size_t)k8n;
+    uint32_t out = 0;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        int src = perm[w * 8 + e];
+        src = src < K ? src : K - 1;
+        out |= ((row[src >> 3] >> (4 * (src & 7))) & 15u) << (4 * e);
+    }
+    qs[i] = out;
+}
+
 }  // namespace
 
 extern "C" {
+
+int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, size_t M, size_t K,
+                      void* st) {
+    const size_t total = M * K;
+    k_gather_cols<<<(unsigned)((total + 255) / 256), 256, 0, S(st)>>>(x, perm, xs, (int)K, total);
+    return snx_launch_check("k_gather_cols");
+}
+
+int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs, size_t N,
+                          size_t K, void* st) {
+    const size_t words = N * (K / 8);
+    k_w4_permute_cols<<<(unsigned)((words + 255) / 256), 256, 0, S(st)>>>(qw, perm, qs, (int)K, words);
+    return snx_launch_check("k_w4_permute_cols");
+}
 
 int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
                   size_t K, void* st) {
@@ -462,18 +567,39 @@ int snx_w4a16_gemv_supported(size_t M, size_t N, size_t K, int group) {
     return M >= 1 && M <= 64 && K % 512 == 0 && group > 0 && group % 128 == 0 && K % group == 0;
 }
 
+size_t snx_w4a16_small_lds(size_t M, size_t K, int perm) {
+    size_t lds = M * (K * 2 + 16) + (K / 128) * 16 + 4 * 64 * 16;
+    if (perm) lds += M * K * 2 + K * 2;   // raw activations + perm
+    return lds;
+}
+
+// The LDS-staged kernel: M <= 4, power-of-two groups, at most 8 items/thread.
+int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
+    return M >= 1 && M <= 4 && K % 512 == 0 && group >= 128 && (group & (group - 1)) == 0 &&
+           K % (size_t)group == 0 && snx_w4a16_small_lds(M, K, perm) <= 65536 &&
+           M * (K / 8) <= 8 * 256;
+}
+
 int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                     const uint32_t* qzeros, void* y, int y_f32, size_t M, size_t N, size_t K,
-                     int group, void* st) {
+                     const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
+                     size_t N, size_t K, int group, void* st) {
     const int G = (int)(K / (size_t)group);
-    const size_t lds = M * (K * 2 + 16) + (K / 128) * 16 + 4 * 64 * 16;
+    const size_t lds = snx_w4a16_small_lds(M, K, perm != NULL);
     const size_t items = M * (K / 8);
-    const bool pow2 = (group & (group - 1)) == 0;
-    if (M <= 4 && pow2 && lds <= 65536 && items <= 8 * 256) {
-        const int m = (int)M, n = (int)N, k = (int)K;
-        if (items <= 2 * 256) return launch_small<2>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
-        if (items <= 4 * 256) return launch_small<4>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
-        return launch_small<8>(x, qw, scales, qzeros, y, y_f32, m, n, k, G, group, lds, S(st));
+    if (snx_w4a16_small_ok(M, K, group, perm != NULL)) {
+        W4Launch a{x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, G, group, lds, S(st)};
+        if (perm) {
+            if (items <= 2 * 256) return launch_small<2, true>(a);
+            if (items <= 4 * 256) return launch_small<4, true>(a);
+            return launch_small<8, true>(a);
+        }
+        if (items <= 2 * 256) return launch_small<2, false>(a);
+        if (items <= 4 * 256) return launch_small<4, false>(a);
+        return launch_small<8, false>(a);
+    }
+    if (perm) {
+        snx_set_error("w4a16 gemv: column-permuted weights need M <= 4 here (M=%zu)", M);
+        return -1;
     }
     if (M <= 16)
         return launch_w4a16<1>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));

@@ -115,14 +115,79 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         size_t ob = y_f32 ? 4 : 2;
         for (size_t m0 = 0; m0 < M; m0 += 64) {
             size_t mm = M - m0 < 64 ? M - m0 : 64;
-            if (snx_k_w4a16_gemv(x + m0 * K, qweight, scales, qzeros, (char*)y + m0 * N * ob,
-                                 y_f32, mm, N, K, group, stream))
+            if (snx_k_w4a16_gemv(x + m0 * K, qweight, scales, qzeros, NULL,
+                                 (char*)y + m0 * N * ob, y_f32, mm, N, K, group, stream))
                 return -1;
         }
         return 0;
     }
     return snx_k_w4a16_generic(x, qweight, scales, qzeros, g_idx, G, y, y_f32, M, N, K, group,
                                stream);
+}
+
+/* Stable counting sort of g_idx on the host (one small copy each way). */
+int SNEPPX_qlinear_w4_actorder_prepare(const uint32_t* qweight, const int32_t* g_idx, size_t G,
+                                       uint32_t* qweight_sorted, uint16_t* perm, size_t N,
+                                       size_t K, SNEPPXStream stream) {
+    REQUIRE(qweight && g_idx && qweight_sorted && perm, "w4_actorder_prepare: NULL pointer");
+    REQUIRE(N && K && G, "w4_actorder_prepare: empty shape");
+    REQUIRE(qweight != qweight_sorted, "w4_actorder_prepare: qweight_sorted must not alias qweight");
+    REQUIRE(K % 8 == 0 && K <= 65536, "w4_actorder_prepare: K=%zu must be a multiple of 8 and <= 65536", K);
+    REQUIRE(K % G == 0, "w4_actorder_prepare: G=%zu must divide K=%zu", G, K);
+    snx_clear_error();
+    const size_t per = K / G;
+    int32_t* h = (int32_t*)malloc(K * sizeof(int32_t));
+    uint16_t* hp = (uint16_t*)malloc(K * sizeof(uint16_t));
+    size_t* next = (size_t*)calloc(G, sizeof(size_t));
+    int rc = (h && hp && next) ? 0 : -1;
+    if (rc) snx_set_error("w4_actorder_prepare: out of host memory");
+    if (!rc) rc = snx_hip_memcpy_d2h(h, g_idx, K * sizeof(int32_t), stream);
+    if (!rc) rc = snx_hip_stream_sync(stream);
+    for (size_t k = 0; !rc && k < K; k++) {
+        if (h[k] < 0 || (size_t)h[k] >= G) {
+            snx_set_error("w4_actorder_prepare: g_idx[%zu]=%d outside [0, %zu)", k, h[k], G);
+            rc = -1;
+        } else if (next[h[k]]++ == per) {
+            snx_set_error("w4_actorder_prepare: group %d holds more than K/G=%zu columns", h[k], per);
+            rc = -1;
+        }
+    }
+    /* every group now holds exactly K/G columns: slot g*per + rank in g */
+    for (size_t g = 0; !rc && g < G; g++) next[g] = g * per;
+    for (size_t k = 0; !rc && k < K; k++) hp[next[h[k]]++] = (uint16_t)k;
+    if (!rc) rc = snx_hip_memcpy_h2d(perm, hp, K * sizeof(uint16_t), stream);
+    if (!rc) rc = snx_k_w4_permute_cols(qweight, perm, qweight_sorted, N, K, stream);
+    if (!rc) rc = snx_hip_stream_sync(stream);
+    free(h);
+    free(hp);
+    free(next);
+    return rc ? -1 : 0;
+}
+
+int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sorted,
+                                  const uint16_t* scales, const uint32_t* qzeros,
+                                  const uint16_t* perm, void* y, SNEPPXDtype y_dtype, size_t M,
+                                  size_t N, size_t K, int group, SNEPPXStream stream) {
+    REQUIRE(x && qweight_sorted && scales && perm && y, "qlinear_w4a16_actorder: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w4a16_actorder: empty shape");
+    REQUIRE(K % 8 == 0 && K <= 65536, "qlinear_w4a16_actorder: K=%zu must be a multiple of 8 and <= 65536", K);
+    REQUIRE(y_dtype == SNEPPX_BFLOAT16 || y_dtype == SNEPPX_FLOAT32,
+            "qlinear_w4a16_actorder: y_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32");
+    REQUIRE(group > 0 && K % (size_t)group == 0,
+            "qlinear_w4a16_actorder: group %d must divide K=%zu", group, K);
+    snx_clear_error();
+    if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) &&
+        snx_w4a16_small_ok(M, K, group, 1))
+        return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y,
+                                y_dtype == SNEPPX_FLOAT32, M, N, K, group, stream);
+    /* other shapes: gather the activation columns once, then the plain path */
+    uint16_t* xs = NULL;
+    if (snx_hip_malloc_async((void**)&xs, M * K * sizeof(uint16_t), stream)) return -1;
+    int rc = snx_k_gather_cols(x, perm, xs, M, K, stream);
+    if (!rc) rc = SNEPPX_qlinear_w4a16(xs, qweight_sorted, scales, qzeros, NULL, 0, y, y_dtype,
+                                       M, N, K, group, stream);
+    if (snx_hip_free_async(xs, stream)) rc = -1;
+    return rc;
 }
 
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,

@@ -73,10 +73,19 @@ int snx_k_w4_gptq_quantize(const float* w, const int32_t* g_idx, size_t G, uint3
 /* ---- linears (gemv_kernels.hip, gemm_kernels.hip) ---- */
 int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y,
                   size_t M, size_t N, size_t K, void* stream);
-/* y_f32: 1 -> fp32 output, 0 -> bf16 */
+/* y_f32: 1 -> fp32 output, 0 -> bf16.  perm (uint16 [K], may be NULL): the
+ * weight columns are stored in that order (M <= 4 only, see small_ok). */
 int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                     const uint32_t* qzeros, void* y, int y_f32, size_t M, size_t N,
-                     size_t K, int group, void* stream);
+                     const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32,
+                     size_t M, size_t N, size_t K, int group, void* stream);
+size_t snx_w4a16_small_lds(size_t M, size_t K, int perm);
+int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm);
+/* xs[m][k'] = x[m][perm[k']] (bf16), perm entries < K */
+int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, size_t M, size_t K,
+                      void* stream);
+/* qs[n] column k' = qw[n] column perm[k'] (packed uint4 words) */
+int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs, size_t N,
+                          size_t K, void* stream);
 /* any group size / g_idx, any M: reference-layout fallback */
 int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,

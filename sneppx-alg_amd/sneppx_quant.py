@@ -71,6 +71,9 @@ EXPORTS = {
     "SNEPPX_qlinear_w8_gemv": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w4a16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, C.c_int, _sz, _sz, _sz,
                                        C.c_int, _vp]),
+    "SNEPPX_qlinear_w4_actorder_prepare": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz,
+                                                C.c_int, _vp]),
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -273,6 +276,20 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w4a16"](
             _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(y), ydt,
             M, N, K, group, self._stream(stream)), "qlinear_w4a16")
+
+    def qlinear_w4_actorder_prepare(self, qweight, g_idx, G, qweight_sorted, perm, stream=None):
+        N, K8 = qweight.shape
+        self.check(self.fn["SNEPPX_qlinear_w4_actorder_prepare"](
+            _ptr(qweight), _ptr(g_idx), G, _ptr(qweight_sorted), _ptr(perm), N, K8 * 8,
+            self._stream(stream)), "qlinear_w4_actorder_prepare")
+
+    def qlinear_w4a16_actorder(self, x, qweight_sorted, scales, qzeros, perm, y, group, stream=None):
+        M, K = x.shape
+        N = qweight_sorted.shape[0]
+        ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_w4a16_actorder"](
+            _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(y), ydt,
+            M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
 
     def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None):
         M, K = A.shape

@@ -191,6 +191,58 @@ def test_w4a16_gptq_actorder(lib, oracle, M):
     assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
 
 
+def _unpack_nibbles(qw, K):
+    q = np.asarray(qw, np.uint32)
+    return np.stack([(q >> (4 * e)) & 15 for e in range(8)], axis=-1).reshape(q.shape[0], K)
+
+
+def test_actorder_prepare_permutes_columns(lib, oracle):
+    N, K = 96, 1024
+    rng = np.random.default_rng(31)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 22, g_idx=g_idx)
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), G, qs, perm)
+    torch.cuda.synchronize()
+    p = perm.cpu().numpy().view(np.uint16).astype(np.int64)
+    assert np.array_equal(p, np.argsort(g_idx, kind="stable"))
+    assert np.array_equal(_unpack_nibbles(qs.cpu().numpy().view(np.uint32), K),
+                          _unpack_nibbles(qw, K)[:, p])
+
+
+def test_actorder_prepare_rejects_uneven_groups(lib, oracle):
+    N, K = 16, 256
+    g_idx = np.zeros(K, np.int32)
+    g_idx[200:] = 1                       # group 0 holds 200 columns, group 1 holds 56
+    qw = np.zeros((N, K // 8), np.uint32)
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    with pytest.raises(Exception, match="columns"):
+        lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), 2, qs, perm)
+
+
+@pytest.mark.parametrize("M,ydt", [(1, torch.float32), (1, torch.bfloat16), (3, torch.float32),
+                                   (4, torch.bfloat16), (8, torch.float32), (300, torch.float32)])
+def test_w4a16_actorder_prepared(lib, oracle, M, ydt):
+    """Prepared (group-contiguous) weights give the layer's result on the
+    original column order: compared with the oracle on qweight + g_idx."""
+    N, K = 1040, 4096
+    rng = np.random.default_rng(40 + M)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 23, g_idx=g_idx)
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), G, qs, perm)
+    y = torch.empty((M, N), dtype=ydt, device=DEV)
+    lib.qlinear_w4a16_actorder(to_dev(x), qs, to_dev(sc), None, perm, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, None, g_idx, N, K, 128)
+    tol = TOL_F32 if ydt == torch.float32 else TOL_BF16
+    assert rel_err(y.float().cpu().numpy(), yo) <= tol
+
+
 def test_w4a16_odd_group_uses_generic_path(lib, oracle):
     N, K, group, M = 30, 96, 32, 2
     qw, sc, qz, G = _w4_case(oracle, N, K, group, 4)
