@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "chain", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -190,6 +190,65 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
             "tops_kernel": ops / mean_launch / 1e9}
 
 
+def llama_tokens(seed=5):
+    """C5 ragged continuous batch: 16 decode rows + 8 prefill chunks of
+    lengths uniform in [32, 512] (seeded), packed into one token matrix."""
+    import numpy as np
+    lens = np.random.RandomState(seed).randint(32, 513, size=8)
+    return 16 + int(lens.sum()), [int(v) for v in lens]
+
+
+def bench_chain(lib, timer, torch, steps, warmup):
+    """C5: one Llama-3-8B decoder layer's linears in W4A16 g128 (AWQ-style,
+    random init): QKV 4096->6144, O 4096->4096, gate/up 4096->2x14336,
+    SiLU(gate)*up, down 14336->4096, on T packed tokens.  The O input is a
+    synthetic bf16 tensor (attention is not part of this path); the gate/up
+    input is the O output."""
+    T, lens = llama_tokens()
+    H, F = 4096, 14336
+    shapes = {"qkv": (6144, H), "o": (H, H), "gate_up": (2 * F, H), "down": (H, F)}
+    g = torch.Generator(device="cuda").manual_seed(17)
+    ws = {}
+    for name, (N, K) in shapes.items():
+        w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+        G = K // 128
+        qw = torch.empty((N, K // 8), dtype=torch.int32, device="cuda")
+        sc = torch.empty((N, G), dtype=torch.int16, device="cuda")
+        qz = torch.empty((N, (G + 7) // 8), dtype=torch.int32, device="cuda")
+        lib.dev_quantize_w4_awq(w, qw, sc, qz, 128)
+        del w
+        ws[name] = (qw, sc, qz, G)
+    x = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
+    attn = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
+    y_qkv = torch.empty((T, 6144), dtype=torch.bfloat16, device="cuda")
+    y_o = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    y_gu = torch.empty((T, 2 * F), dtype=torch.bfloat16, device="cuda")
+    act = torch.empty((T, F), dtype=torch.bfloat16, device="cuda")
+    y_d = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    st = timer.stream
+
+    def lin(name, inp, out):
+        qw, sc, qz, G = ws[name]
+        lib.qlinear_w4a16(inp, qw, sc, qz, None, G, out, 128, stream=st)
+
+    def layer():
+        lin("qkv", x, y_qkv)
+        lin("o", attn, y_o)
+        lin("gate_up", y_o, y_gu)
+        lib.qlinear_silu_mul(y_gu, act, stream=st)
+        lin("down", act, y_d)
+
+    total, _, _ = timer.run([layer], steps, warmup)
+    per = {}
+    for name, inp, out in (("qkv", x, y_qkv), ("o", attn, y_o), ("gate_up", y_o, y_gu), ("down", act, y_d)):
+        t, _, _ = timer.run([lambda n=name, i=inp, o=out: lin(n, i, o)], steps, 2)
+        N, K = shapes[name]
+        per[name] = {"us": round(t / steps * 1e3, 1), "tflops": round(2 * T * N * K / (t / steps) / 1e9, 1)}
+    flops = 2 * T * sum(N * K for N, K in shapes.values())
+    return {"T": T, "chunk_lens": lens, "flops": flops, "ms_per_step": total / steps,
+            "tflops": flops / (total / steps) / 1e9, "per_linear": per}
+
+
 def cpu_baseline(ws_host, x_host, N, K, group, seconds):
     """The oracle's C restatement (C2 GEMV: dequantise + k-ascending fp32 dot,
     the reference tensor.c:1820-1823 order), one host thread, -O3."""
@@ -237,6 +296,9 @@ def run_only(args, lib, timer, torch, N, K, group):
     elif args.only in ("gemm-i8", "gemm-fp8"):
         r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, steps, 2, fp8=args.only == "gemm-fp8")
         print(f"{args.only}: {r['ms_per_step'] * 1e3:.1f} us/launch, {r['tops']:.0f} TOPS")
+    elif args.only == "chain":
+        r = bench_chain(lib, timer, torch, steps, 2)
+        print(f"chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s {r['per_linear']}")
     else:
         # a plain device copy of known size, the calibration for FETCH/WRITE_SIZE
         n = 256 << 20
@@ -299,6 +361,14 @@ def main():
         extra.append({"workload": "C1 W8 weight-only GEMV N=4096 K=4096 M=1 fp32", "value": round(r["gbs"], 1),
                       "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                       "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
+        r = bench_chain(lib, timer, torch, 10, 2)
+        extra.append({"workload": f"C5 Llama-3-8B layer W4A16 g128 linear chain T={r['T']} "
+                                  f"(16 decode + 8 prefill chunks {r['chunk_lens']})",
+                      "value": round(r["tflops"], 1), "unit": "TFLOP/s",
+                      "frac_of_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
+                      "ms_per_step": round(r["ms_per_step"], 4), "per_linear": r["per_linear"]})
+        print(f"[bench] C5 chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s",
+              file=sys.stderr, flush=True)
         for fp8 in (False, True):
             r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, 10, 2, fp8=fp8)
             peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS

@@ -105,6 +105,13 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
                                   const uint16_t* perm, void* y, SNEPPXDtype y_dtype,
                                   size_t M, size_t N, size_t K, int group, SNEPPXStream stream);
 
+/* C5 SwiGLU step between the gate/up and down projections (no reference
+ * counterpart; the reference's MLP is fp32): gate_up bf16 [T][2F] with gate
+ * in columns [0, F) and up in [F, 2F); out bf16 [T][F] =
+ * bf16(g / (1 + exp(-g)) * u) computed in fp32.  F % 8 == 0. */
+int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
+                            SNEPPXStream stream);
+
 /* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n]), acc = sum_k A*W in
  * int32 (exact).  A int8 [M][K] (per-token scales sA fp32 [M]), W int8 [N][K]
  * (per-channel sW fp32 [N]), out bf16 [M][N]. */

@@ -1,0 +1,331 @@
+// w4_gemm_kernels.hip - W4A16 prefill GEMM for gfx950 (MFMA-bound, bf16).
+//
+// y[m][n] = sum_k x[m][k] * (q[n][k] - z[n][g]) * s[n][g],  g = k / group,
+// fp32 accumulation, for large M (prefill / continuous batches).
+//
+//  1. k_w4_prep_x: one pass over the activations writes them in the MFMA
+//     k-slot order the weight unpack produces ({0,4,1,5,2,6,3,7} within every
+//     8 columns) and the fp32 sums X[g128][m] of every 128-column step.
+//  2. k_w4a16_gemm: 128x256 output tiles, 8 waves (2 along M x 4 along N,
+//     64x64 each = 4x4 blocks of v_mfma_f32_16x16x32_bf16), K step 128.
+//     Activation and packed-weight tiles move global->LDS with
+//     global_load_lds_dwordx4 (double-buffered, 2 x 48 KB).  Activation rows
+//     are 256 B; their 16-byte chunks are XOR-swizzled by (row & 15), so the
+//     16 rows of a fragment read 16 different chunks (no bank conflicts).
+//     Weight rows are 64 B and a fragment read covers 1 KB contiguous.
+//     Nibbles become bf16 (128 + q) with one v_and_or_b32 per pair; after each
+//     128-column step the accumulator block is folded into the fp32 result:
+//     y += s * acc - s * (128 + z) * X  (exact bias/zero-point removal).
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "codec.h"
+#include "../snx_internal.h"
+
+using namespace snx;
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+constexpr int GBM = 128, GBN = 256, GBK = 128;
+constexpr int GFM = 4, GFN = 4;                 // 16x16 blocks per wave along M, N
+constexpr int GLDS_A = GBM * GBK * 2;           // 32 KB of bf16 activations
+constexpr int GLDS_B = GBN * GBK / 2;           // 16 KB of packed weights
+constexpr int GLDS_X = GBM * 4;                 // fp32 step sums of the tile's rows
+constexpr int GLDS_STAGE = GLDS_A + GLDS_B + GLDS_X;
+
+// ---------------------------------------------------------------- prep pass
+// One thread per 8 columns.  K % 128 == 0, so the 16 threads of one
+// 128-column step are 16 consecutive lanes.
+__global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ x,
+                                                   uint16_t* __restrict__ xp,
+                                                   float* __restrict__ xs, int K, int Mp,
+                                                   size_t items) {
+    const size_t it = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const bool live = it < items;
+    const size_t itc = live ? it : items - 1;
+    const int k8n = K >> 3;
+    const int m = (int)(itc / (size_t)k8n);
+    const int k8 = (int)(itc - (size_t)m * k8n);
+    const u32x4 v = *reinterpret_cast<const u32x4*>(x + itc * 8);
+    u32x4 p;
+    p[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+    p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+    p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+    p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+    if (live) *reinterpret_cast<u32x4*>(xp + itc * 8) = p;
+    float sum = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        sum += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xFFFF0000u);
+    sum += __shfl_xor(sum, 8);
+    sum += __shfl_xor(sum, 4);
+    sum += __shfl_xor(sum, 2);
+    sum += __shfl_xor(sum, 1);
+    if (live && (k8 & 15) == 0) xs[(size_t)(k8 >> 4) * Mp + m] = sum;
+}
+
+// ----------------------------------------------------------------- the GEMM
+template <bool ZEROS, bool YF32>
+__global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
+                                                    const float* __restrict__ xs,
+                                                    const uint32_t* __restrict__ qw,
+                                                    const uint16_t* __restrict__ scales,
+                                                    const uint32_t* __restrict__ qz,
+                                                    void* __restrict__ y, int M, int N, int K,
+                                                    int G, int gshift, int Mp, int tiles_m) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 2, wn = wave & 3;
+    const int r16 = lane & 15, q = lane >> 4;
+
+    // XCD-aware order: consecutive tiles of one M-row of tiles share an XCD
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * GBM, n0 = tn * GBN;
+
+    // direct-load sources (byte offsets; operands < 4 GiB).  A: wave w,
+    // instruction i fills 1 KB block 8 i + w = tile rows 4 blk .. 4 blk + 3,
+    // lane -> (row, LDS chunk)
+    const uint32_t krow = (uint32_t)K * 2;      // bytes per activation row
+    const uint32_t wrowb = (uint32_t)K / 2;     // bytes per packed weight row
+    uint32_t ga[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (8 * i + wave) * 4 + (lane >> 4);
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        const int chunk = (lane & 15) ^ (row & 15);
+        ga[i] = (uint32_t)gr * krow + (uint32_t)chunk * 16u;
+    }
+    // W: 16 rows per 1 KB block, 4 lanes per 64-byte row
+    uint32_t gw[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int row = (8 * i + wave) * 16 + (lane >> 2);
+        const int gn = n0 + row < N ? n0 + row : N - 1;
+        gw[i] = (uint32_t)gn * wrowb + (uint32_t)(lane & 3) * 16u;
+    }
+    const uint8_t* xpb = reinterpret_cast<const uint8_t*>(xp);
+    const uint8_t* qwb = reinterpret_cast<const uint8_t*>(qw);
+    auto dload = [&](int buf, int kt) {
+        uint8_t* base = lds + buf * GLDS_STAGE;
+        const uint32_t ka = (uint32_t)kt * (GBK * 2), kw = (uint32_t)kt * (GBK / 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds(xpb + (ga[i] + ka), base + (8 * i + wave) * 1024, 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            __builtin_amdgcn_global_load_lds(qwb + (gw[i] + kw), base + GLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
+        if (wave < 2)   // the step sums of the tile's 128 rows
+            __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + wave * 64 + lane,
+                                             base + GLDS_A + GLDS_B + wave * 256, 4, 0, 0);
+    };
+
+    // per-lane epilogue operands: columns n of the 4 n-blocks
+    int ncol[GFN];
+#pragma unroll
+    for (int j = 0; j < GFN; j++) {
+        const int n = n0 + wn * 64 + j * 16 + r16;
+        ncol[j] = n < N ? n : N - 1;
+    }
+    const int zw = (G + 7) >> 3;
+    const int mrow = m0 + wm * 64 + q * 4;       // + 16 i + e
+    auto fetch = [&](int kt, uint32_t* sr, uint32_t* zr) {
+        const int g = (kt * GBK) >> gshift;
+#pragma unroll
+        for (int j = 0; j < GFN; j++) {
+            sr[j] = scales[(size_t)ncol[j] * G + g];
+            zr[j] = ZEROS ? qz[(size_t)ncol[j] * zw + (g >> 3)] : 0u;
+        }
+    };
+
+    f32x4 yacc[GFM][GFN];
+#pragma unroll
+    for (int i = 0; i < GFM; i++)
+#pragma unroll
+        for (int j = 0; j < GFN; j++) yacc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    uint32_t nib_mask, bf_bias;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
+
+    const int nk = K / GBK;
+    const uint8_t* arow = lds + (wm * 64 + r16) * (GBK * 2);
+    const uint8_t* wrow = lds + GLDS_A + (wn * 64 + r16) * (GBK / 2) + q * 16;
+
+    uint32_t sr[GFN], zr[GFN];
+    dload(0, 0);
+    fetch(0, sr, zr);
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0070);   // stage kt and its scales landed
+        __syncthreads();                      // and every wave is done with the other buffer
+        uint32_t sn[GFN], zn[GFN];
+        const int kn = kt + 1 < nk ? kt + 1 : kt;   // last stage: reload itself, unused
+        dload(cur ^ 1, kn);
+        fetch(kn, sn, zn);
+
+        const uint8_t* ab = arow + cur * GLDS_STAGE;
+        const uint8_t* wb = wrow + cur * GLDS_STAGE;
+        u32x4 wv[GFN];
+#pragma unroll
+        for (int j = 0; j < GFN; j++) wv[j] = *reinterpret_cast<const u32x4*>(wb + j * 16 * (GBK / 2));
+        f32x4 acc[GFM][GFN];
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            bf16x8 fa[GFM], fb[GFN];
+#pragma unroll
+            for (int i = 0; i < GFM; i++)
+                fa[i] = *reinterpret_cast<const bf16x8*>(ab + i * 16 * (GBK * 2) + (((4 * q + s) ^ r16) << 4));
+#pragma unroll
+            for (int j = 0; j < GFN; j++) {
+                const uint32_t w = wv[j][s];
+                u32x4 bq;
+                bq[0] = (w & nib_mask) | bf_bias;
+                bq[1] = ((w >> 4) & nib_mask) | bf_bias;
+                bq[2] = ((w >> 8) & nib_mask) | bf_bias;
+                bq[3] = ((w >> 12) & nib_mask) | bf_bias;
+                fb[j] = __builtin_bit_cast(bf16x8, bq);
+            }
+#pragma unroll
+            for (int i = 0; i < GFM; i++)
+#pragma unroll
+                for (int j = 0; j < GFN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        fa[i], fb[j], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j], 0, 0, 0);
+        }
+        // fold this 128-column step: y += s*acc - s*(128+z)*X
+        const int g = (kt * GBK) >> gshift;
+        const float* xb = reinterpret_cast<const float*>(lds + cur * GLDS_STAGE + GLDS_A + GLDS_B) + wm * 64 + q * 4;
+        f32x4 xr[GFM];
+#pragma unroll
+        for (int i = 0; i < GFM; i++) xr[i] = *reinterpret_cast<const f32x4*>(xb + i * 16);
+#pragma unroll
+        for (int j = 0; j < GFN; j++) {
+            const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)sr[j]);
+            const uint32_t z = ZEROS ? (zr[j] >> (4 * (g & 7))) & 15u : 8u;
+            const float nc = -sf * (float)(128u + z);
+#pragma unroll
+            for (int i = 0; i < GFM; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    yacc[i][j][e] = __builtin_fmaf(nc, xr[i][e], __builtin_fmaf(sf, acc[i][j][e], yacc[i][j][e]));
+        }
+#pragma unroll
+        for (int j = 0; j < GFN; j++) {
+            sr[j] = sn[j];
+            zr[j] = zn[j];
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < GFM; i++) {
+#pragma unroll
+        for (int j = 0; j < GFN; j++) {
+            const int n = n0 + wn * 64 + j * 16 + r16;
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = mrow + i * 16 + e;
+                if (m >= M) continue;
+                if (YF32)
+                    reinterpret_cast<float*>(y)[(size_t)m * N + n] = yacc[i][j][e];
+                else
+                    reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = bf16_out(yacc[i][j][e]);
+            }
+        }
+    }
+}
+
+template <bool ZEROS, bool YF32>
+int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                   const uint16_t* scales, const uint32_t* qz, void* y, int M, int N, int K,
+                   int group, int Mp, hipStream_t st) {
+    const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
+    const size_t lds = 2 * (size_t)GLDS_STAGE;
+    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+        attr_set = true;
+    }
+    const int gshift = __builtin_ctz((unsigned)group);
+    k_w4a16_gemm<ZEROS, YF32><<<tiles_m * tiles_n, 512, lds, st>>>(
+        xp, xs, qw, scales, qz, y, M, N, K, K / group, gshift, Mp, tiles_m);
+    return snx_launch_check("k_w4a16_gemm");
+}
+
+// SiLU(gate) * up between the gate/up and down projections of a SwiGLU MLP:
+// gu [T][2F] bf16 (gate in columns [0, F), up in [F, 2F)), out [T][F] bf16,
+// out = bf16(g / (1 + exp(-g)) * u) in fp32.  One thread per 8 columns.
+__global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ gu,
+                                                  uint16_t* __restrict__ out, int F, size_t items) {
+    const size_t it = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (it >= items) return;
+    const int f8n = F >> 3;
+    const size_t t = it / (size_t)f8n;
+    const int f = (int)(it - t * (size_t)f8n) * 8;
+    const u32x4 gv = *reinterpret_cast<const u32x4*>(gu + t * (size_t)(2 * F) + f);
+    const u32x4 uv = *reinterpret_cast<const u32x4*>(gu + t * (size_t)(2 * F) + F + f);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        const float g0 = __builtin_bit_cast(float, gv[e] << 16), g1 = __builtin_bit_cast(float, gv[e] & 0xFFFF0000u);
+        const float u0 = __builtin_bit_cast(float, uv[e] << 16), u1 = __builtin_bit_cast(float, uv[e] & 0xFFFF0000u);
+        const float r0 = g0 / (1.0f + expf(-g0)) * u0;
+        const float r1 = g1 / (1.0f + expf(-g1)) * u1;
+        o[e] = (uint32_t)bf16_out(r0) | (uint32_t)bf16_out(r1) << 16;
+    }
+    *reinterpret_cast<u32x4*>(out + t * (size_t)F + f) = o;
+}
+
+}  // namespace
+
+extern "C" {
+
+int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* st) {
+    const size_t items = T * (F / 8);
+    k_silu_mul<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(gu, out, (int)F, items);
+    return snx_launch_check("k_silu_mul");
+}
+
+
+size_t snx_w4_prep_rows(size_t M) { return (M + GBM - 1) / GBM * GBM; }
+
+int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group) {
+    return M >= 1 && N >= 1 && K >= GBK && K % GBK == 0 && group >= GBK &&
+           (group & (group - 1)) == 0 && K % (size_t)group == 0 && M * K * 2 < (1ull << 32) &&
+           N * K / 2 < (1ull << 32);
+}
+
+int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,
+                    void* st) {
+    const size_t items = M * (K / 8);
+    k_w4_prep_x<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(x, xp, xs, (int)K, (int)Mp, items);
+    return snx_launch_check("k_w4_prep_x");
+}
+
+int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                     const uint16_t* scales, const uint32_t* qzeros, void* y, int y_f32,
+                     size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
+    const int m = (int)M, n = (int)N, k = (int)K, mp = (int)Mp;
+    if (qzeros) {
+        if (y_f32) return launch_w4_gemm<true, true>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+        return launch_w4_gemm<true, false>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+    }
+    if (y_f32) return launch_w4_gemm<false, true>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+    return launch_w4_gemm<false, false>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+}
+
+}  // extern "C"

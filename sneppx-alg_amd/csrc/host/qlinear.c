@@ -10,6 +10,9 @@
 #include "snx_hip.h"
 #include "../snx_internal.h"
 
+/* rows from which W4A16 runs the MFMA GEMM instead of 64-row GEMV slices */
+#define SNX_W4_GEMM_MIN_M 256
+
 static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 #define REQUIRE(cond, ...)               \
@@ -109,6 +112,22 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         G = K / (size_t)group;
     }
     snx_clear_error();
+    if (!g_idx && M >= SNX_W4_GEMM_MIN_M && aligned16(x) && aligned16(qweight) &&
+        snx_w4a16_gemm_ok(M, N, K, group)) {
+        /* prefill GEMM: activations prepared once into a stream-ordered workspace */
+        const size_t Mp = snx_w4_prep_rows(M);
+        const size_t xp_bytes = (M * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+        char* ws = NULL;
+        if (snx_hip_malloc_async((void**)&ws, xp_bytes + (K / 128) * Mp * sizeof(float), stream))
+            return -1;
+        uint16_t* xp = (uint16_t*)ws;
+        float* xs = (float*)(ws + xp_bytes);
+        int rc = snx_k_w4_prep_x(x, xp, xs, M, K, Mp, stream);
+        if (!rc) rc = snx_k_w4a16_gemm(xp, xs, qweight, scales, qzeros, y, y_f32, M, N, K, group,
+                                       Mp, stream);
+        if (snx_hip_free_async(ws, stream)) rc = -1;
+        return rc;
+    }
     if (!g_idx && aligned16(x) && aligned16(qweight) &&
         snx_w4a16_gemv_supported(M < 64 ? M : 64, N, K, group)) {
         /* decode GEMV; larger M in 64-row slices that reuse each weight load */
@@ -188,6 +207,16 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
                                        M, N, K, group, stream);
     if (snx_hip_free_async(xs, stream)) rc = -1;
     return rc;
+}
+
+int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
+                            SNEPPXStream stream) {
+    REQUIRE(gate_up && out, "qlinear_silu_mul: NULL pointer");
+    REQUIRE(T && F, "qlinear_silu_mul: empty shape");
+    REQUIRE(F % 8 == 0, "qlinear_silu_mul: F=%zu must be a multiple of 8", F);
+    REQUIRE(aligned16(gate_up) && aligned16(out), "qlinear_silu_mul: buffers must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_silu_mul(gate_up, out, T, F, stream);
 }
 
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,

@@ -92,6 +92,19 @@ int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* s
                         int y_f32, size_t M, size_t N, size_t K, int group, void* stream);
 int snx_w4a16_gemv_supported(size_t M, size_t N, size_t K, int group);
 
+/* W4A16 prefill GEMM (w4_gemm_kernels.hip): activations prepared once
+ * (k-slot order + fp32 sums per 128 columns, xs [K/128][Mp]), then the GEMM. */
+size_t snx_w4_prep_rows(size_t M);
+int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group);
+int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,
+                    void* stream);
+int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                     const uint16_t* scales, const uint32_t* qzeros, void* y, int y_f32,
+                     size_t M, size_t N, size_t K, int group, size_t Mp, void* stream);
+
+/* SwiGLU step: out [T][F] = bf16(silu(gu[:, :F]) * gu[:, F:]), F % 8 == 0 */
+int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* stream);
+
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
                   int32_t* c_i32, uint16_t* out_bf16, size_t M, size_t N, size_t K,
                   void* stream);

@@ -74,6 +74,7 @@ EXPORTS = {
     "SNEPPX_qlinear_w4_actorder_prepare": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz,
                                                 C.c_int, _vp]),
+    "SNEPPX_qlinear_silu_mul": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -290,6 +291,11 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w4a16_actorder"](
             _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(y), ydt,
             M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
+
+    def qlinear_silu_mul(self, gate_up, out, stream=None):
+        T, F2 = gate_up.shape
+        self.check(self.fn["SNEPPX_qlinear_silu_mul"](
+            _ptr(gate_up), _ptr(out), T, F2 // 2, self._stream(stream)), "qlinear_silu_mul")
 
     def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None):
         M, K = A.shape

@@ -243,6 +243,51 @@ def test_w4a16_actorder_prepared(lib, oracle, M, ydt):
     assert rel_err(y.float().cpu().numpy(), yo) <= tol
 
 
+# ------------------------------------------------------ W4A16 prefill GEMM
+@pytest.mark.parametrize("M,N,K,group,sym,out", [
+    (256, 512, 1024, 128, False, "f32"),     # whole tiles
+    (300, 1000, 512, 256, True, "f32"),      # M and N tails, group 256, symmetric
+    (257, 256, 4096, 128, False, "bf16"),    # one row into the second M tile
+    (600, 136, 2048, 512, False, "f32"),     # N narrower than one tile, group 512
+])
+def test_w4a16_gemm(lib, oracle, M, N, K, group, sym, out):
+    print(f"[gpu] w4a16 gemm M={M} N={N} K={K} g={group} sym={sym} out={out}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, 50 + M, sym=sym)
+    x = bf16_bits(np.random.default_rng(60 + M).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None if qz is None else to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
+@pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (600, 4096, 14336)])
+def test_w4a16_gemm_llama_shapes_sampled_rows(lib, oracle, M, N, K):
+    """Full-size QKV (T=2192) and down-projection shapes: weights quantized on
+    the GPU (bit-exact quantizer), every output row of a sample checked
+    against the oracle, including the last, partial M tile."""
+    print(f"[gpu] w4a16 gemm llama M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M)
+    w = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    G = K // 128
+    qw = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    sc = torch.empty((N, G), dtype=torch.int16, device=DEV)
+    qz = torch.empty((N, (G + 7) // 8), dtype=torch.int32, device=DEV)
+    lib.dev_quantize_w4_awq(w, qw, sc, qz, 128)
+    del w
+    x = torch.randn((M, K), device=DEV, generator=g).to(torch.bfloat16)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(x, qw, sc, qz, None, G, y, 128)
+    torch.cuda.synchronize()
+    rows = np.array(sorted({0, 1, 63, 64, 127, 128, 255, M // 2, M - 129, M - 17, M - 2, M - 1}))
+    xh = u16(x)[rows]
+    rc, yo = oracle.w4a16_linear(xh, qw.cpu().numpy().view(np.uint32), u16(sc),
+                                 qz.cpu().numpy().view(np.uint32), None, N, K, 128)
+    got = bf16_to_f32(u16(y)[rows])
+    assert rel_err(got, yo) <= TOL_BF16
+
+
 def test_w4a16_odd_group_uses_generic_path(lib, oracle):
     N, K, group, M = 30, 96, 32, 2
     qw, sc, qz, G = _w4_case(oracle, N, K, group, 4)
@@ -312,3 +357,19 @@ def test_fp8_gemm(lib, oracle, M, N, K):
     torch.cuda.synchronize()
     ref = oracle.fp8_gemm(ca, cw, sa, sw)
     assert rel_err(bf16_to_f32(u16(out)), ref) <= TOL_BF16
+
+
+# ------------------------------------------------------------ SwiGLU step
+@pytest.mark.parametrize("T,F", [(1, 8), (37, 14336), (300, 1000)])
+def test_silu_mul(lib, T, F):
+    rng = np.random.default_rng(T)
+    gu = bf16_bits(rng.normal(0, 2, (T, 2 * F)).astype(np.float32))
+    out = torch.empty((T, F), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_silu_mul(to_dev(gu), out)
+    torch.cuda.synchronize()
+    g = bf16_to_f32(gu[:, :F]).astype(np.float64)
+    u = bf16_to_f32(gu[:, F:]).astype(np.float64)
+    want = g / (1.0 + np.exp(-g)) * u
+    got = bf16_to_f32(u16(out)).astype(np.float64)
+    # one bf16 rounding of the fp32 value: |err| <= 2^-8 |want| (+ fp32 slack)
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
