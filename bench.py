@@ -40,7 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "chain", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -296,6 +296,21 @@ def run_only(args, lib, timer, torch, N, K, group):
     elif args.only in ("gemm-i8", "gemm-fp8"):
         r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, steps, 2, fp8=args.only == "gemm-fp8")
         print(f"{args.only}: {r['ms_per_step'] * 1e3:.1f} us/launch, {r['tops']:.0f} TOPS")
+    elif args.only == "gemm-w4":
+        # the chain's widest linear alone (gate/up, 4096 -> 2 x 14336)
+        T, _ = llama_tokens()
+        N2, K2 = 28672, 4096
+        w = torch.randn((N2, K2), device="cuda") * 0.02
+        qw = torch.empty((N2, K2 // 8), dtype=torch.int32, device="cuda")
+        sc = torch.empty((N2, K2 // 128), dtype=torch.int16, device="cuda")
+        qz = torch.empty((N2, K2 // 1024), dtype=torch.int32, device="cuda")
+        lib.dev_quantize_w4_awq(w, qw, sc, qz, 128)
+        del w
+        x = torch.randn((T, K2), device="cuda").to(torch.bfloat16)
+        y = torch.empty((T, N2), dtype=torch.bfloat16, device="cuda")
+        st = timer.stream
+        t, _, _ = timer.run([lambda: lib.qlinear_w4a16(x, qw, sc, qz, None, K2 // 128, y, 128, stream=st)], steps, 2)
+        print(f"gemm-w4 T={T} N={N2} K={K2}: {t / steps * 1e3:.1f} us, {2 * T * N2 * K2 / (t / steps) / 1e9:.0f} TFLOP/s")
     elif args.only == "chain":
         r = bench_chain(lib, timer, torch, steps, 2)
         print(f"chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s {r['per_linear']}")

@@ -38,7 +38,6 @@ constexpr int GFM = 4, GFN = 4;                 // 16x16 blocks per wave along M
 constexpr int GLDS_A = GBM * GBK * 2;           // 32 KB of bf16 activations
 constexpr int GLDS_B = GBN * GBK / 2;           // 16 KB of packed weights
 constexpr int GLDS_X = GBM * 4;                 // fp32 step sums of the tile's rows
-constexpr int GLDS_STAGE = GLDS_A + GLDS_B + GLDS_X;
 
 // ---------------------------------------------------------------- prep pass
 // One thread per 8 columns.  K % 128 == 0, so the 16 threads of one
@@ -72,6 +71,22 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
 }
 
 // ----------------------------------------------------------------- the GEMM
+// LDS ring of three stages (one K step of 128 columns each):
+//   A   128 rows x 256 B  bf16 activations, chunk c of row r at c ^ (r & 15)
+//   B   256 rows x 64 B   packed weights,   chunk c of row r at c ^ bsw(r)
+//   X   128 fp32          step sums of the tile's rows
+//   S   256 u32           fp16 scale pair (g & ~1, g | 1) of every tile column
+//   Z   256 u32           zero-point word of every tile column
+// Every wave issues exactly 8 direct loads per stage, so "stage kt landed"
+// is vmcnt(8) while stage kt + 1 is still in flight.
+constexpr int GOFF_B = GLDS_A, GOFF_X = GOFF_B + GLDS_B, GOFF_S = GOFF_X + GLDS_X;
+constexpr int GOFF_Z = GOFF_S + GBN * 4, GRING = GOFF_Z + GBN * 4;
+constexpr int GSTAGES = 3;
+
+// 64-byte weight rows: rows 2 and 4 apart share banks, so each row's four
+// 16-byte chunks rotate by bits 1-3 of the row (conflict-free 16-lane reads)
+__device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
 template <bool ZEROS, bool YF32>
 __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
                                                     const float* __restrict__ xs,
@@ -111,40 +126,35 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     for (int i = 0; i < 2; i++) {
         const int row = (8 * i + wave) * 16 + (lane >> 2);
         const int gn = n0 + row < N ? n0 + row : N - 1;
-        gw[i] = (uint32_t)gn * wrowb + (uint32_t)(lane & 3) * 16u;
+        gw[i] = (uint32_t)gn * wrowb + (uint32_t)((lane & 3) ^ bsw(row)) * 16u;
     }
+    // scales (waves 0-3) or zero words (waves 4-7) of tile column 64 (w&3) + lane;
+    // without zero points waves 4-7 repeat the scale load (same bytes, same slot)
+    const int scol = n0 + 64 * (wave & 3) + lane;
+    const int sn = scol < N ? scol : N - 1;
+    const bool zload = ZEROS && wave >= 4;
+    const int zw = (G + 7) >> 3;
     const uint8_t* xpb = reinterpret_cast<const uint8_t*>(xp);
     const uint8_t* qwb = reinterpret_cast<const uint8_t*>(qw);
     auto dload = [&](int buf, int kt) {
-        uint8_t* base = lds + buf * GLDS_STAGE;
+        uint8_t* base = lds + buf * GRING;
         const uint32_t ka = (uint32_t)kt * (GBK * 2), kw = (uint32_t)kt * (GBK / 2);
+        const int g = (kt * GBK) >> gshift;
 #pragma unroll
         for (int i = 0; i < 4; i++)
             __builtin_amdgcn_global_load_lds(xpb + (ga[i] + ka), base + (8 * i + wave) * 1024, 16, 0, 0);
 #pragma unroll
         for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_global_load_lds(qwb + (gw[i] + kw), base + GLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
-        if (wave < 2)   // the step sums of the tile's 128 rows
-            __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + wave * 64 + lane,
-                                             base + GLDS_A + GLDS_B + wave * 256, 4, 0, 0);
-    };
-
-    // per-lane epilogue operands: columns n of the 4 n-blocks
-    int ncol[GFN];
-#pragma unroll
-    for (int j = 0; j < GFN; j++) {
-        const int n = n0 + wn * 64 + j * 16 + r16;
-        ncol[j] = n < N ? n : N - 1;
-    }
-    const int zw = (G + 7) >> 3;
-    const int mrow = m0 + wm * 64 + q * 4;       // + 16 i + e
-    auto fetch = [&](int kt, uint32_t* sr, uint32_t* zr) {
-        const int g = (kt * GBK) >> gshift;
-#pragma unroll
-        for (int j = 0; j < GFN; j++) {
-            sr[j] = scales[(size_t)ncol[j] * G + g];
-            zr[j] = ZEROS ? qz[(size_t)ncol[j] * zw + (g >> 3)] : 0u;
-        }
+            __builtin_amdgcn_global_load_lds(qwb + (gw[i] + kw), base + GOFF_B + (8 * i + wave) * 1024, 16, 0, 0);
+        if (zload)
+            __builtin_amdgcn_global_load_lds(qz + (size_t)sn * zw + (g >> 3),
+                                             base + GOFF_Z + 256 * (wave & 3), 4, 0, 0);
+        else
+            __builtin_amdgcn_global_load_lds(scales + (size_t)sn * G + (g & ~1),
+                                             base + GOFF_S + 256 * (wave & 3), 4, 0, 0);
+        // step sums of the tile's 128 rows (each half loaded by four waves)
+        __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + (wave & 1) * 64 + lane,
+                                         base + GOFF_X + (wave & 1) * 256, 4, 0, 0);
     };
 
     f32x4 yacc[GFM][GFN];
@@ -158,27 +168,52 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
 
     const int nk = K / GBK;
+    const int mrow = m0 + wm * 64 + q * 4;       // + 16 i + e
     const uint8_t* arow = lds + (wm * 64 + r16) * (GBK * 2);
-    const uint8_t* wrow = lds + GLDS_A + (wn * 64 + r16) * (GBK / 2) + q * 16;
+    const uint8_t* wrow = lds + GOFF_B + (wn * 64 + r16) * (GBK / 2) + ((q ^ bsw(r16)) << 4);
 
+    // fold one 128-column step into the result: y += s*acc - s*(128+z)*X
+    auto fold = [&](const f32x4 (&acc)[GFM][GFN], const f32x4* xr, const uint32_t* sr,
+                    const uint32_t* zr, int g) {
+#pragma unroll
+        for (int j = 0; j < GFN; j++) {
+            const uint16_t h = (uint16_t)(sr[j] >> (16 * (g & 1)));
+            const float sf = (float)__builtin_bit_cast(_Float16, h);
+            const uint32_t z = ZEROS ? (zr[j] >> (4 * (g & 7))) & 15u : 8u;
+            const float nc = -sf * (float)(128u + z);
+#pragma unroll
+            for (int i = 0; i < GFM; i++)
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    yacc[i][j][e] = __builtin_fmaf(nc, xr[i][e], __builtin_fmaf(sf, acc[i][j][e], yacc[i][j][e]));
+        }
+    };
+
+    // The two waves that share a SIMD (w and w + 4) run half a step apart:
+    // waves 4..7 fold a step after the next barrier, while waves 0..3 issue
+    // that step's MFMAs, and the other way round at the end of the step, so
+    // the fp32 fold of one wave overlaps the MFMAs of the other.
+    const bool late = wave >= 4;
     uint32_t sr[GFN], zr[GFN];
+    f32x4 xr[GFM];
+    f32x4 acc[GFM][GFN];
+    int gp = 0;
     dload(0, 0);
-    fetch(0, sr, zr);
+    dload(1, nk > 1 ? 1 : 0);
     for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt & 1;
-        __builtin_amdgcn_s_waitcnt(0x0070);   // stage kt and its scales landed
-        __syncthreads();                      // and every wave is done with the other buffer
-        uint32_t sn[GFN], zn[GFN];
-        const int kn = kt + 1 < nk ? kt + 1 : kt;   // last stage: reload itself, unused
-        dload(cur ^ 1, kn);
-        fetch(kn, sn, zn);
+        const int cur = kt % GSTAGES;
+        __builtin_amdgcn_s_waitcnt(0x0078);   // vmcnt(8): stage kt landed, kt + 1 may fly
+        __syncthreads();                      // and every wave is done with stage kt - 1
+        __builtin_amdgcn_sched_barrier(0);    // nothing below moves above the wait
+        const int kn = kt + 2 < nk ? kt + 2 : nk - 1;   // past the end: reload, unused
+        dload((kt + 2) % GSTAGES, kn);
+        if (late && kt > 0) fold(acc, xr, sr, zr, gp);
 
-        const uint8_t* ab = arow + cur * GLDS_STAGE;
-        const uint8_t* wb = wrow + cur * GLDS_STAGE;
+        const uint8_t* ab = arow + cur * GRING;
+        const uint8_t* wb = wrow + cur * GRING;
         u32x4 wv[GFN];
 #pragma unroll
         for (int j = 0; j < GFN; j++) wv[j] = *reinterpret_cast<const u32x4*>(wb + j * 16 * (GBK / 2));
-        f32x4 acc[GFM][GFN];
 #pragma unroll
         for (int s = 0; s < 4; s++) {
             bf16x8 fa[GFM], fb[GFN];
@@ -202,29 +237,26 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
                         fa[i], fb[j], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j], 0, 0, 0);
         }
-        // fold this 128-column step: y += s*acc - s*(128+z)*X
-        const int g = (kt * GBK) >> gshift;
-        const float* xb = reinterpret_cast<const float*>(lds + cur * GLDS_STAGE + GLDS_A + GLDS_B) + wm * 64 + q * 4;
-        f32x4 xr[GFM];
+        // this step's sums, scales and zero words (the ring slot is refilled
+        // after the next barrier, so the late waves keep them in registers)
+        const uint8_t* st = lds + cur * GRING;
+        const float* xb = reinterpret_cast<const float*>(st + GOFF_X) + wm * 64 + q * 4;
 #pragma unroll
         for (int i = 0; i < GFM; i++) xr[i] = *reinterpret_cast<const f32x4*>(xb + i * 16);
 #pragma unroll
         for (int j = 0; j < GFN; j++) {
-            const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)sr[j]);
-            const uint32_t z = ZEROS ? (zr[j] >> (4 * (g & 7))) & 15u : 8u;
-            const float nc = -sf * (float)(128u + z);
-#pragma unroll
-            for (int i = 0; i < GFM; i++)
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    yacc[i][j][e] = __builtin_fmaf(nc, xr[i][e], __builtin_fmaf(sf, acc[i][j][e], yacc[i][j][e]));
+            const int c = wn * 64 + j * 16 + r16;
+            sr[j] = reinterpret_cast<const uint32_t*>(st + GOFF_S)[c];
+            zr[j] = ZEROS ? reinterpret_cast<const uint32_t*>(st + GOFF_Z)[c] : 0u;
         }
-#pragma unroll
-        for (int j = 0; j < GFN; j++) {
-            sr[j] = sn[j];
-            zr[j] = zn[j];
-        }
+        const int g = (kt * GBK) >> gshift;
+        if (!late)
+            fold(acc, xr, sr, zr, g);
+        else
+            gp = g;
     }
+    if (late) fold(acc, xr, sr, zr, gp);
+    __builtin_amdgcn_s_waitcnt(0x0070);   // the ring's last (unused) loads drain before exit
 
 #pragma unroll
     for (int i = 0; i < GFM; i++) {
@@ -250,7 +282,7 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                    const uint16_t* scales, const uint32_t* qz, void* y, int M, int N, int K,
                    int group, int Mp, hipStream_t st) {
     const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
-    const size_t lds = 2 * (size_t)GLDS_STAGE;
+    const size_t lds = (size_t)GSTAGES * GRING;
     static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
     if (!attr_set) {
         if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32>),
@@ -304,9 +336,10 @@ int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* 
 size_t snx_w4_prep_rows(size_t M) { return (M + GBM - 1) / GBM * GBM; }
 
 int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group) {
+    // the stage loads read fp16 scales in aligned pairs: an even group count
     return M >= 1 && N >= 1 && K >= GBK && K % GBK == 0 && group >= GBK &&
-           (group & (group - 1)) == 0 && K % (size_t)group == 0 && M * K * 2 < (1ull << 32) &&
-           N * K / 2 < (1ull << 32);
+           (group & (group - 1)) == 0 && K % (size_t)group == 0 && (K / group) % 2 == 0 &&
+           M * K * 2 < (1ull << 32) && N * K / 2 < (1ull << 32);
 }
 
 int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,

@@ -113,6 +113,7 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
     }
     snx_clear_error();
     if (!g_idx && M >= SNX_W4_GEMM_MIN_M && aligned16(x) && aligned16(qweight) &&
+        ((uintptr_t)scales & 3u) == 0 && ((uintptr_t)qzeros & 3u) == 0 &&
         snx_w4a16_gemm_ok(M, N, K, group)) {
         /* prefill GEMM: activations prepared once into a stream-ordered workspace */
         const size_t Mp = snx_w4_prep_rows(M);
