@@ -40,6 +40,7 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
+    p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
     p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
@@ -291,8 +292,8 @@ def run_only(args, lib, timer, torch, N, K, group):
     """One kernel family, for profiler passes (prints one line, no JSON)."""
     steps = args.steps
     if args.only == "gemv":
-        r, _ = bench_w4a16(lib, timer, torch, 1, N, K, group, args.copies, steps, args.warmup)
-        print(f"gemv C2 M=1: {r['ms_per_step'] * 1e3:.3f} us/launch, {r['gbs']:.0f} GB/s")
+        r, _ = bench_w4a16(lib, timer, torch, args.m, N, K, group, args.copies, steps, args.warmup)
+        print(f"gemv C2 M={args.m}: {r['ms_per_step'] * 1e3:.3f} us/launch, {r['gbs']:.0f} GB/s")
     elif args.only in ("gemm-i8", "gemm-fp8"):
         r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, steps, 2, fp8=args.only == "gemm-fp8")
         print(f"{args.only}: {r['ms_per_step'] * 1e3:.1f} us/launch, {r['tops']:.0f} TOPS")

@@ -401,6 +401,146 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     }
 }
 
+// Split-K W4A16 for 5 <= M <= 16: workgroup (bx, s) owns output rows
+// [64 bx, +64) (16 per wave) and the K span [s kspan, +kspan).  It stages
+// only that span of the M activation rows in LDS (slot order, per-step
+// sums), so the four waves share one copy, and every wave streams its 16
+// weight rows across the span with all of its loads in flight at once.
+// MFMA rows beyond M read zeros.  Partial sums go to part[s][M][N] (fp32);
+// k_w4a16_reduce adds the S partials in a fixed order.
+template <bool ZEROS>
+__global__ void __launch_bounds__(256) k_w4a16_splitk(const uint16_t* __restrict__ x,
+                                                      const uint32_t* __restrict__ qw,
+                                                      const uint16_t* __restrict__ scales,
+                                                      const uint32_t* __restrict__ qz,
+                                                      float* __restrict__ part, int M, int N,
+                                                      int K, int G, int gshift, int kspan) {
+    constexpr int CH = 8;                                       // steps per wave (kspan <= 1024)
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const int xrow = kspan * 2 + 16;                            // bytes per staged row (+pad)
+    float* xsum = reinterpret_cast<float*>(smem + 16 * xrow);   // [steps][16]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nl = lane & 15, kq = lane >> 4;
+    const int n0 = blockIdx.x * 64 + wave * 16;
+    const int n = n0 + nl < N ? n0 + nl : N - 1;
+    const int s = blockIdx.y, kb = s * kspan;
+    const int steps = kspan >> 7;
+    const int k8n = K >> 3, zw = (G + 7) >> 3;
+    const int span8 = kspan >> 3, nitems = M * span8;           // <= 8 items per thread
+
+    // 1. activation items of the span (L2-resident after the first workgroups)
+    u32x4 xr[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int it = tid + i * 256;
+        it = it < nitems ? it : nitems - 1;
+        const int m = it / span8;
+        xr[i] = load16(x + (size_t)m * K + kb + (it - m * span8) * 8);
+    }
+    asm volatile("" ::: "memory");
+    // 2. scales / zeros, 3. weights: every step of the span in flight
+    uint32_t sreg[CH], zreg[CH];
+    u32x4 wv[CH];
+    const uint32_t* wrow = qw + (size_t)n * k8n + (kb >> 3) + kq * 4;
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        const int st = c < steps ? c : steps - 1;
+        const int g = (kb + st * 128) >> gshift;
+        sreg[c] = scales[(size_t)n * G + g];
+        zreg[c] = ZEROS ? qz[(size_t)n * zw + (g >> 3)] : 0u;
+    }
+#pragma unroll
+    for (int c = 0; c < CH; c++) wv[c] = load16(wrow + (c < steps ? c : steps - 1) * 16);
+    asm volatile("" ::: "memory");
+
+    // stage the span in slot order 0,4,1,5,2,6,3,7 and sum every 128 columns
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int it = tid + i * 256;
+        const bool live = it < nitems;
+        const int itc = live ? it : nitems - 1;
+        const int m = itc / span8;
+        const int k8 = itc - m * span8;
+        const int off = live ? m * xrow + k8 * 16 : 16 * xrow - 16;   // dead items: pad slot
+        u32x4 p;
+        p[0] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x05040100u);
+        p[1] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x07060302u);
+        p[2] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x05040100u);
+        p[3] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x07060302u);
+        *reinterpret_cast<u32x4*>(smem + off) = p;
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            sum += __builtin_bit_cast(float, xr[i][e] << 16) + __builtin_bit_cast(float, xr[i][e] & 0xFFFF0000u);
+        sum += __shfl_xor(sum, 8);
+        sum += __shfl_xor(sum, 4);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 1);
+        if (live && (k8 & 15) == 0) xsum[(k8 >> 4) * 16 + m] = sum;
+    }
+    __syncthreads();
+
+    uint32_t nib_mask, bf_bias;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
+
+    const bool arow = nl < M;
+    const uint8_t* abase = smem + (arow ? nl : 0) * xrow + kq * 64;
+    f32x4 yacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < CH; c++) {
+        if (c >= steps) break;
+        const int g = (kb + c * 128) >> gshift;
+        u32x4 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) a[j] = u32x4{0u, 0u, 0u, 0u};
+        if (arow) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) a[j] = *reinterpret_cast<const u32x4*>(abase + c * 256 + j * 16);
+        }
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t w = wv[c][j];
+            u32x4 b;
+            b[0] = (w & nib_mask) | bf_bias;
+            b[1] = ((w >> 4) & nib_mask) | bf_bias;
+            b[2] = ((w >> 8) & nib_mask) | bf_bias;
+            b[3] = ((w >> 12) & nib_mask) | bf_bias;
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a[j]),
+                                                          __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+        }
+        const float sf = (float)__builtin_bit_cast(_Float16, (uint16_t)sreg[c]);
+        const uint32_t z = ZEROS ? (zreg[c] >> (4 * (g & 7))) & 15u : 8u;
+        const float corr = sf * (float)(128u + z);
+        const f32x4 xs = *reinterpret_cast<const f32x4*>(xsum + c * 16 + kq * 4);
+#pragma unroll
+        for (int i = 0; i < 4; i++) yacc[i] += sf * acc[i] - corr * xs[i];
+    }
+    if (n0 + nl >= N) return;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {   // MFMA C layout: row 4 (lane/16) + i, column lane % 16
+        const int m = kq * 4 + i;
+        if (m < M) part[((size_t)s * M + m) * N + n0 + nl] = yacc[i];
+    }
+}
+
+// y[m][n] = sum over s of part[s][m][n], s ascending
+__global__ void __launch_bounds__(256) k_w4a16_reduce(const float* __restrict__ part,
+                                                      void* __restrict__ y, int y_f32, int S,
+                                                      size_t MN) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= MN) return;
+    float v = 0.0f;
+    for (int s = 0; s < S; s++) v += part[(size_t)s * MN + i];
+    if (y_f32)
+        reinterpret_cast<float*>(y)[i] = v;
+    else
+        reinterpret_cast<uint16_t*>(y)[i] = f32_to_bf16(v);
+}
+
 struct W4Launch {
     const uint16_t* x;
     const uint32_t* qw;
@@ -535,6 +675,36 @@ __global__ void __launch_bounds__(256) k_w4_permute_cols(const uint32_t* __restr
 }  // namespace
 
 extern "C" {
+
+int snx_w4a16_splitk_span(size_t M, size_t K, int group) {
+    if (M < 1 || M > 16 || K % 128 != 0 || group < 128 || (group & (group - 1)) != 0 ||
+        K % (size_t)group != 0)
+        return 0;
+    const size_t steps = K / 128;
+    for (size_t d = 8; d >= 1; d--)
+        if (steps % d == 0) return (int)(d * 128);
+    return 0;
+}
+
+int snx_k_w4a16_splitk(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                       const uint32_t* qzeros, float* part, size_t M, size_t N, size_t K,
+                       int group, int kspan, void* st) {
+    const int G = (int)(K / (size_t)group), gshift = __builtin_ctz((unsigned)group);
+    const size_t lds = 16 * ((size_t)kspan * 2 + 16) + (size_t)(kspan / 128) * 16 * 4;
+    dim3 grid((unsigned)((N + 63) / 64), (unsigned)(K / (size_t)kspan));
+    if (qzeros)
+        k_w4a16_splitk<true><<<grid, 256, lds, S(st)>>>(x, qw, scales, qzeros, part, (int)M, (int)N,
+                                                        (int)K, G, gshift, kspan);
+    else
+        k_w4a16_splitk<false><<<grid, 256, lds, S(st)>>>(x, qw, scales, qzeros, part, (int)M, (int)N,
+                                                         (int)K, G, gshift, kspan);
+    return snx_launch_check("k_w4a16_splitk");
+}
+
+int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S_, size_t MN, void* st) {
+    k_w4a16_reduce<<<(unsigned)((MN + 255) / 256), 256, 0, S(st)>>>(part, y, y_f32, S_, MN);
+    return snx_launch_check("k_w4a16_reduce");
+}
 
 int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, size_t M, size_t K,
                       void* st) {

@@ -2,6 +2,11 @@
 // the library's thread-local error text.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+#include <cstdint>
+#include <mutex>
+#include <vector>
+
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -52,15 +57,74 @@ int snx_hip_malloc(void** ptr, size_t bytes) {
 
 int snx_hip_free(void* ptr) { return ptr ? check(hipFree(ptr), "hipFree") : 0; }
 
+// The library's workspaces come from the device's default stream-ordered
+// pool.  With the pool's default release threshold (0) its memory goes back
+// to the driver at every synchronisation, so each call would map fresh
+// memory; keeping it (threshold = max) makes a workspace allocation a cheap
+// pool operation.  Set once per device.
+static int keep_pool_memory() {
+    static std::atomic<uint64_t> done{0};   // bit d: device d configured
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    const uint64_t bit = 1ull << dev;
+    if (done.load(std::memory_order_acquire) & bit) return 0;
+    hipMemPool_t pool;
+    if (hipDeviceGetDefaultMemPool(&pool, dev) == hipSuccess) {
+        uint64_t keep = UINT64_MAX;
+        (void)hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep);
+    }
+    done.fetch_or(bit, std::memory_order_acq_rel);
+    return 0;
+}
+
 int snx_hip_malloc_async(void** ptr, size_t bytes, void* stream) {
     if (!ptr) return -1;
     *ptr = nullptr;
     if (bytes == 0) bytes = 1;
+    keep_pool_memory();
     return check(hipMallocAsync(ptr, bytes, S(stream)), "hipMallocAsync");
 }
 
 int snx_hip_free_async(void* ptr, void* stream) {
     return ptr ? check(hipFreeAsync(ptr, S(stream)), "hipFreeAsync") : 0;
+}
+
+// Workspaces kept per (device, stream, slot) for the library's internal
+// scratch (split-K partials, prepared activations, gathers).  Work on one
+// stream runs in order, so a call may reuse its stream's buffer without
+// waiting; a larger request releases the old buffer stream-ordered (after
+// the work already queued on that stream) and takes a new one from the pool.
+namespace {
+struct Workspace {
+    int dev, slot;
+    void* stream;
+    void* ptr;
+    size_t bytes;
+};
+std::mutex g_ws_mu;
+std::vector<Workspace> g_ws;
+}  // namespace
+
+void* snx_workspace(size_t bytes, int slot, void* stream) {
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    if (bytes == 0) bytes = 1;
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    Workspace* w = nullptr;
+    for (auto& e : g_ws)
+        if (e.dev == dev && e.slot == slot && e.stream == stream) w = &e;
+    if (w && w->bytes >= bytes) return w->ptr;
+    const size_t want = (bytes + (bytes >> 2) + 4095) & ~(size_t)4095;   // +25% headroom
+    void* p = nullptr;
+    if (snx_hip_malloc_async(&p, want, stream)) return nullptr;
+    if (w) {
+        if (snx_hip_free_async(w->ptr, stream)) return nullptr;
+        w->ptr = p;
+        w->bytes = want;
+    } else {
+        g_ws.push_back(Workspace{dev, slot, stream, p, want});
+    }
+    return p;
 }
 
 int snx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {

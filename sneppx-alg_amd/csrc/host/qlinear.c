@@ -72,15 +72,13 @@ int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* sc
     REQUIRE(n, "dev_quantize_fp8_e4m3_scaled: n == 0");
     snx_clear_error();
     int parts = snx_reduce_parts(n);
-    float* ws = NULL;
-    if (snx_hip_malloc_async((void**)&ws, ((size_t)parts * 2 + 64) * sizeof(float), stream))
-        return -1;
+    float* ws = (float*)snx_workspace(((size_t)parts * 2 + 64) * sizeof(float), 0, stream);
+    if (!ws) return -1;
     float* rec = ws + (size_t)parts * 2;
     rec = (float*)(((uintptr_t)rec + 15u) & ~(uintptr_t)15u);
     int rc = snx_k_absmax(in, n, ws, parts, stream);
     if (!rc) rc = snx_k_finalize_scale(ws, parts, SNX_SCALE_FP8_240, in, rec, scale_out, stream);
     if (!rc) rc = snx_k_fp8_encode(in, out, n, 0, rec, stream);
-    if (snx_hip_free_async(ws, stream)) rc = -1;
     return rc;
 }
 
@@ -118,15 +116,23 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         /* prefill GEMM: activations prepared once into a stream-ordered workspace */
         const size_t Mp = snx_w4_prep_rows(M);
         const size_t xp_bytes = (M * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-        char* ws = NULL;
-        if (snx_hip_malloc_async((void**)&ws, xp_bytes + (K / 128) * Mp * sizeof(float), stream))
-            return -1;
+        char* ws = (char*)snx_workspace(xp_bytes + (K / 128) * Mp * sizeof(float), 1, stream);
+        if (!ws) return -1;
         uint16_t* xp = (uint16_t*)ws;
         float* xs = (float*)(ws + xp_bytes);
         int rc = snx_k_w4_prep_x(x, xp, xs, M, K, Mp, stream);
         if (!rc) rc = snx_k_w4a16_gemm(xp, xs, qweight, scales, qzeros, y, y_f32, M, N, K, group,
                                        Mp, stream);
-        if (snx_hip_free_async(ws, stream)) rc = -1;
+        return rc;
+    }
+    const int kspan = snx_w4a16_splitk_span(M, K, group);
+    if (!g_idx && M > 4 && kspan && aligned16(x) && aligned16(qweight)) {
+        /* 5 <= M <= 16: split-K decode + ordered reduction of the partials */
+        const size_t S = K / (size_t)kspan;
+        float* part = (float*)snx_workspace(S * M * N * sizeof(float), 1, stream);
+        if (!part) return -1;
+        int rc = snx_k_w4a16_splitk(x, qweight, scales, qzeros, part, M, N, K, group, kspan, stream);
+        if (!rc) rc = snx_k_w4a16_reduce(part, y, y_f32, (int)S, M * N, stream);
         return rc;
     }
     if (!g_idx && aligned16(x) && aligned16(qweight) &&
@@ -201,12 +207,11 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
         return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y,
                                 y_dtype == SNEPPX_FLOAT32, M, N, K, group, stream);
     /* other shapes: gather the activation columns once, then the plain path */
-    uint16_t* xs = NULL;
-    if (snx_hip_malloc_async((void**)&xs, M * K * sizeof(uint16_t), stream)) return -1;
+    uint16_t* xs = (uint16_t*)snx_workspace(M * K * sizeof(uint16_t), 0, stream);
+    if (!xs) return -1;
     int rc = snx_k_gather_cols(x, perm, xs, M, K, stream);
     if (!rc) rc = SNEPPX_qlinear_w4a16(xs, qweight_sorted, scales, qzeros, NULL, 0, y, y_dtype,
                                        M, N, K, group, stream);
-    if (snx_hip_free_async(xs, stream)) rc = -1;
     return rc;
 }
 

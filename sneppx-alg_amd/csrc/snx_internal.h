@@ -15,6 +15,9 @@ extern "C" {
 #endif
 
 void snx_set_error(const char* fmt, ...);
+/* device scratch reused by every call on (current device, stream, slot);
+ * slot 1 is for a call made from inside another one.  NULL on failure. */
+void* snx_workspace(size_t bytes, int slot, void* stream);
 void snx_clear_error(void);
 int snx_launch_check(const char* kernel);
 
@@ -80,6 +83,13 @@ int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scal
                      size_t M, size_t N, size_t K, int group, void* stream);
 size_t snx_w4a16_small_lds(size_t M, size_t K, int perm);
 int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm);
+/* split-K decode (5 <= M <= 16): K span per workgroup (0 = unsupported),
+ * partials part [K/kspan][M][N] fp32, then the ordered reduction */
+int snx_w4a16_splitk_span(size_t M, size_t K, int group);
+int snx_k_w4a16_splitk(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                       const uint32_t* qzeros, float* part, size_t M, size_t N, size_t K,
+                       int group, int kspan, void* stream);
+int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S, size_t MN, void* stream);
 /* xs[m][k'] = x[m][perm[k']] (bf16), perm entries < K */
 int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, size_t M, size_t K,
                       void* stream);

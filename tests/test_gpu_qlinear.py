@@ -243,6 +243,24 @@ def test_w4a16_actorder_prepared(lib, oracle, M, ydt):
     assert rel_err(y.float().cpu().numpy(), yo) <= tol
 
 
+@pytest.mark.parametrize("M,N,K,group,sym,out", [
+    (5, 11008, 4096, 128, False, "f32"),     # split-K decode, 4 spans of 1024
+    (8, 1000, 1408, 128, True, "f32"),       # 11 steps: spans of 128, N tail
+    (12, 64, 4096, 256, False, "bf16"),      # one row block, group 256
+    (16, 4096, 14336, 128, False, "f32"),    # down-projection width
+])
+def test_w4a16_splitk_decode(lib, oracle, M, N, K, group, sym, out):
+    print(f"[gpu] w4a16 split-K M={M} N={N} K={K} g={group} sym={sym} out={out}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, 70 + M, sym=sym)
+    x = bf16_bits(np.random.default_rng(80 + M).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None if qz is None else to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
 # ------------------------------------------------------ W4A16 prefill GEMM
 @pytest.mark.parametrize("M,N,K,group,sym,out", [
     (256, 512, 1024, 128, False, "f32"),     # whole tiles
