@@ -76,6 +76,71 @@ __global__ void __launch_bounds__(256) k_w8_gemv(const float* __restrict__ x,
     }
 }
 
+// M = 1, K = 1024 SL: a workgroup of 4 waves stages x (fp32) once in LDS;
+// each wave owns R rows and issues all R x SL of its 16-byte weight loads
+// (lane l: bytes [16 l, +16) of every 1 KB slice) before the first FMA.
+// Bytes are read as unsigned (b ^ 0x80 = b + 128) with v_cvt_f32_ubyte*,
+// and 128 * sum(x) is taken off at the end:
+// sum x*b = sum x*(b + 128) - 128 * sum x.
+template <int R, int SL>
+__global__ void __launch_bounds__(256) k_w8_gemv1(const float* __restrict__ x,
+                                                  const int8_t* __restrict__ q,
+                                                  const float* __restrict__ s,
+                                                  float* __restrict__ y, int N, int K) {
+    extern __shared__ __attribute__((aligned(16))) float xl[];   // [K]
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int n0 = (blockIdx.x * 4 + wave) * R;
+
+    float4 xr[SL];   // x: K / 4 float4 = SL per thread
+#pragma unroll
+    for (int i = 0; i < SL; i++) xr[i] = reinterpret_cast<const float4*>(x)[tid + 256 * i];
+    asm volatile("" ::: "memory");
+    u32x4 w[R][SL];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int n = n0 + r < N ? n0 + r : N - 1;
+#pragma unroll
+        for (int sl = 0; sl < SL; sl++) w[r][sl] = load16(q + (size_t)n * K + sl * 1024 + lane * 16);
+    }
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < SL; i++) reinterpret_cast<float4*>(xl)[tid + 256 * i] = xr[i];
+    __syncthreads();
+
+    float acc[R], xsum = 0.0f;
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+#pragma unroll
+    for (int sl = 0; sl < SL; sl++) {
+        float xv[16];
+#pragma unroll
+        for (int t = 0; t < 16; t += 4) {
+            const float4 v = reinterpret_cast<const float4*>(xl + sl * 1024 + lane * 16)[t >> 2];
+            xv[t] = v.x; xv[t + 1] = v.y; xv[t + 2] = v.z; xv[t + 3] = v.w;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; t++) xsum += xv[t];
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t u = w[r][sl][e] ^ 0x80808080u;
+                // (float)(byte j of u) compiles to one v_cvt_f32_ubyte<j>
+                acc[r] += xv[4 * e] * (float)(u & 0xFFu);
+                acc[r] += xv[4 * e + 1] * (float)((u >> 8) & 0xFFu);
+                acc[r] += xv[4 * e + 2] * (float)((u >> 16) & 0xFFu);
+                acc[r] += xv[4 * e + 3] * (float)(u >> 24);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = wave_sum(acc[r] - 128.0f * xsum);
+        if (lane == 0 && n0 + r < N) y[n0 + r] = s[n0 + r] * v;
+    }
+}
+
 // Any K: one wave per row, scalar tail.
 __global__ void __launch_bounds__(256) k_w8_gemv_any(const float* __restrict__ x,
                                                      const int8_t* __restrict__ q,
@@ -722,6 +787,16 @@ int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs
 
 int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
                   size_t K, void* st) {
+    if (M == 1 && (K == 1024 || K == 2048 || K == 4096 || K == 8192)) {
+        const size_t lds = K * sizeof(float);
+        const unsigned rows_per_wg = K <= 4096 ? 16 : 8;   // R = 4 (2 at K = 8192)
+        const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
+        if (K == 1024) k_w8_gemv1<4, 1><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
+        else if (K == 2048) k_w8_gemv1<4, 2><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
+        else if (K == 4096) k_w8_gemv1<4, 4><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
+        else k_w8_gemv1<2, 8><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
+        return snx_launch_check("k_w8_gemv1");
+    }
     if (K % 16 == 0) {
         constexpr int R = 4;
         size_t waves = (N + R - 1) / R;
