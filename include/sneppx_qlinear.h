@@ -48,6 +48,17 @@ const char* SNEPPX_qlinear_last_error(void);
 int SNEPPX_dev_quantize_int8_channel(const float* in, int8_t* q, float* scales,
                                      size_t rows, size_t cols, SNEPPXStream stream);
 
+/* Rounding of the quantizers' x * (1/scale).  SNEPPX_ROUND_HALF_AWAY is the
+ * reference's roundf (quantize_int8.c:61,172) and the default everywhere;
+ * SNEPPX_ROUND_HALF_EVEN is offered for callers that specify ties to even. */
+typedef enum { SNEPPX_ROUND_HALF_AWAY = 0, SNEPPX_ROUND_HALF_EVEN = 1 } SNEPPXRounding;
+
+/* SNEPPX_dev_quantize_int8_channel with a choice of rounding (no reference
+ * counterpart for SNEPPX_ROUND_HALF_EVEN); scales are identical in both. */
+int SNEPPX_dev_quantize_int8_channel_rounding(const float* in, int8_t* q, float* scales,
+                                              size_t rows, size_t cols, SNEPPXRounding rounding,
+                                              SNEPPXStream stream);
+
 /* W4 AWQ-style asymmetric uint4 (build-defined, generalises
  * quantize_int8.c:98-123 to 4 bits with a stored fp16 scale):
  * per (row, group): s = fp16((max-min)/15), z = clamp(roundf(-min/s), 0, 15),

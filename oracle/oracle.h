@@ -52,6 +52,8 @@ int orc_quantize_int8_asym(const float* in, int8_t* out, size_t n,
                            float* scale_out, int32_t* zp_out);
 int orc_dequantize_int8_asym(const int8_t* in, float* out, size_t n,
                              float scale, int32_t zp);
+int orc_quantize_int8_channel_rne(const float* in, int8_t* out, size_t rows, size_t cols,
+                                  float* scales_out);
 int orc_quantize_int8_channel(const float* in, int8_t* out, size_t rows,
                               size_t cols, float* scales_out);
 int orc_quantize_int4_sym(const float* in, uint8_t* out, size_t n, float* scale_out);

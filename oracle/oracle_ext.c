@@ -323,3 +323,30 @@ void orc_fp8_gemm(const uint8_t* A, const uint8_t* W, float sA, float sW,
             out[m * N + n] = acc * sA * sW;
         }
 }
+
+/* Build-defined option (no reference counterpart): the per-row int8
+ * quantizer of quantize_int8.c:157-177 with ties to even instead of roundf.
+ * Scales are the reference's.  Pinned against numpy's rint (half-even) on the
+ * same fp32 products x * (1/s). */
+int orc_quantize_int8_channel_rne(const float* in, int8_t* out, size_t rows, size_t cols,
+                                  float* scales_out)
+{
+    if (!in || !out || !scales_out || rows == 0 || cols == 0) return -1;
+    for (size_t r = 0; r < rows; r++) {
+        const float* x = in + r * cols;
+        float m = 0.0f;
+        for (size_t c = 0; c < cols; c++) {
+            float a = fabsf(x[c]);
+            if (a > m) m = a;
+        }
+        float s = (m < FLT_MIN) ? 1.0f : m / 127.0f;
+        float inv = 1.0f / s;
+        scales_out[r] = s;
+        for (size_t c = 0; c < cols; c++) {
+            float v = rintf(x[c] * inv);
+            int32_t q = (v >= -2147483648.0f && v < 2147483648.0f) ? (int32_t)v : INT32_MIN;
+            out[r * cols + c] = (int8_t)clampi(q, -128, 127);
+        }
+    }
+    return 0;
+}

@@ -71,6 +71,7 @@ _COMMON = {
 }
 
 _ORACLE_ONLY = {
+    "quantize_int8_channel_rne": (C.c_int, [_f32p, _i8p, _sz, _sz, _f32p]),
     "gptq_quantize_literal": _COMMON["gptq_quantize"],
     "fake_quant": (C.c_int, [_f32p, _f32p, _sz, C.c_float, C.c_int]),
     "matmul_kn": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz]),
@@ -141,6 +142,14 @@ class _Lib:
         q = np.zeros((rows, cols), np.int8)
         s = np.zeros(rows, np.float32)
         rc = self.raw["quantize_int8_channel"](x, q, rows, cols, s)
+        return rc, q, s
+
+    def quantize_int8_channel_rne(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        rows, cols = x.shape
+        q = np.zeros((rows, cols), np.int8)
+        s = np.zeros(rows, np.float32)
+        rc = self.raw["quantize_int8_channel_rne"](x, q, rows, cols, s)
         return rc, q, s
 
     def quantize_int4_sym(self, x):

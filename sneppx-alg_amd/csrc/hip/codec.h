@@ -20,6 +20,14 @@ SNX_HD int32_t round_i32(float v) {
     return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
 }
 
+// The same conversion with ties to even (rintf under the default rounding
+// mode): the "round-half-even" reading of the C1 config, offered as an
+// explicit option next to the reference's roundf.
+SNX_HD int32_t rne_i32(float v) {
+    float r = rintf(v);
+    return (r >= -2147483648.0f && r < 2147483648.0f) ? (int32_t)r : INT32_MIN;
+}
+
 SNX_HD int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }

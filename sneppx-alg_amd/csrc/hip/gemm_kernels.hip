@@ -472,6 +472,189 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
     }
 }
 
+// int8 on the 32x32 shape: same tile, LDS layout and direct loads as
+// k_gemm_8w, but the 8 waves split the tile along M only (wave w owns rows
+// [32 w, +32) and all 224 columns = 7 blocks of 32x32), so a stage issues
+// 28 v_mfma_i32_32x32x32_i8 per wave -- half the instructions of the 16x16
+// shape for the same work.  Operand lane l: row (A) / column (W) l % 32,
+// k-bytes [16 (l/32), +16) of each 32-byte k-step.
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+constexpr int XCROW = 232;   // u16 per staged output row: 224 + 8 pad
+static_assert(8 * 32 * XCROW * 2 <= 2 * TLDS_STAGE, "output staging fits in the LDS ring");
+
+template <bool FP8, bool RAW>
+__global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
+                                                    const int8_t* __restrict__ W,
+                                                    const float* __restrict__ sA,
+                                                    const float* __restrict__ sW,
+                                                    int32_t* __restrict__ Craw,
+                                                    uint16_t* __restrict__ out, int M, int N,
+                                                    int K, int tiles_m, int tiles_n) {
+    constexpr int FN = TBN / 32;                 // 7 blocks per wave
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r32 = lane & 31, h = lane >> 5;
+
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * TBM, n0 = tn * TBN;
+
+    const int lrow = lane >> 3, lslot = lane & 7;
+    uint32_t ga[4], gw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (8 * i + wave) * 8 + lrow;
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
+        const int wr = row < TBN ? row : TBN - 1;
+        const int gn = n0 + wr < N ? n0 + wr : N - 1;
+        gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
+    }
+    auto dload = [&](int buf, int k0) {
+        int8_t* base = lds + buf * TLDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
+        if (wave < 4)
+            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
+    };
+
+    typedef typename std::conditional<FP8, f32x16, i32x16>::type acc_t;
+    acc_t acc[FN];
+#pragma unroll
+    for (int j = 0; j < FN; j++) acc[j] = acc_t{};
+
+    const int sw = swz(r32);
+    const int8_t* arow = lds + (wave * 32 + r32) * TBK;
+    const int8_t* wrow = lds + TLDS_A + r32 * TBK;
+    const int nk = K / TBK;
+
+    dload(0, 0);
+    float sa[16], swv[FN];
+    if (!RAW) {
+#pragma unroll
+        for (int v = 0; v < 16; v++) {
+            const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+            sa[v] = FP8 ? sA[0] : sA[m < M ? m : M - 1];
+        }
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + j * 32 + r32;
+            swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
+        }
+    }
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+        dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
+        const int8_t* ab = arow + cur * TLDS_STAGE;
+        const int8_t* wb = wrow + cur * TLDS_STAGE;
+        if (!FP8) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {          // k-steps of 32 bytes: chunk 2 s + h
+                const int off = ((2 * s + h) ^ sw) << 4;
+                const i32x4 fa = lds16(ab + off);
+                i32x4 fw[FN];
+#pragma unroll
+                for (int j = 0; j < FN; j++) fw[j] = lds16(wb + j * 32 * TBK + off);
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[j] = (acc_t)__builtin_amdgcn_mfma_i32_32x32x32_i8(fa, fw[j], (i32x16)acc[j], 0, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < 2; s++) {          // k-steps of 64 bytes: chunks 4 s + 2 h, +1
+                const int o0 = ((4 * s + 2 * h) ^ sw) << 4, o1 = ((4 * s + 2 * h + 1) ^ sw) << 4;
+                const i32x4 alo = lds16(ab + o0), ahi = lds16(ab + o1);
+                const i32x8 fa = i32x8{alo[0], alo[1], alo[2], alo[3], ahi[0], ahi[1], ahi[2], ahi[3]};
+                i32x8 fw[FN];
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    const i32x4 lo = lds16(wb + j * 32 * TBK + o0), hi = lds16(wb + j * 32 * TBK + o1);
+                    fw[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+                    acc[j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                        fa, fw[j], (f32x16)acc[j], 0, 0, 0, 0, 0, 0);
+            }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // the last (unused) loads drain before exit
+
+    if (RAW) {   // int32 accumulators (bit-exactness checks): direct stores
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + j * 32 + r32;
+            if (n >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {    // 32x32 C layout: row 8 (v/4) + 4 (l/32) + v%4
+                const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (m < M) Craw[(size_t)m * N + n] = ((i32x16)acc[j])[v];
+            }
+        }
+        return;
+    }
+    // bf16 tile through LDS: each wave writes its 32 x 224 block row-major
+    // (rows padded to 464 B: the two lane halves, 4 rows apart, use different
+    // banks), then stores 16-byte pieces, 448 contiguous bytes per row.
+    __syncthreads();                      // every wave is done with the ring
+    uint16_t* ct = reinterpret_cast<uint16_t*>(lds) + wave * (32 * XCROW);
+#pragma unroll
+    for (int j = 0; j < FN; j++)
+#pragma unroll
+        for (int v = 0; v < 16; v++)
+            ct[(8 * (v >> 2) + 4 * h + (v & 3)) * XCROW + j * 32 + r32] =
+                bf16_out((float)acc[j][v] * sa[v] * swv[j]);
+    const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+    for (int t = 0; t < 14; t++) {        // 32 rows x 28 pieces = 896 = 14 x 64
+        const int qd = t * 64 + lane;
+        const int row = qd / 28, c = qd - row * 28;
+        const int m = m0 + wave * 32 + row, n = n0 + c * 8;
+        if (m >= M || n >= N) continue;
+        const i32x4 val = *reinterpret_cast<const i32x4*>(ct + row * XCROW + c * 8);
+        uint16_t* dst = out + (size_t)m * N + n;
+        if (vec && n + 8 <= N) {
+            *reinterpret_cast<i32x4*>(dst) = val;
+        } else {
+            const uint16_t* e = reinterpret_cast<const uint16_t*>(&val);
+            for (int i = 0; i < 8 && n + i < N; i++) dst[i] = e[i];
+        }
+    }
+}
+
+template <bool FP8, bool RAW>
+int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
+                 int32_t* Craw, uint16_t* out, int M, int N, int K, hipStream_t st) {
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+    if ((uint64_t)M * K >= (1ull << 32) || (uint64_t)N * K >= (1ull << 32)) {
+        snx_set_error("gemm: operands above 4 GiB are not supported");
+        return -1;
+    }
+    const size_t lds = 2 * (size_t)TLDS_STAGE;
+    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_x32<FP8, RAW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+        attr_set = true;
+    }
+    k_gemm_x32<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
+                                                          tiles_m, tiles_n);
+    return snx_launch_check("k_gemm_x32");
+}
+
 template <bool FP8, bool RAW>
 int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
                  uint16_t* out, int M, int N, int K, hipStream_t st) {
@@ -507,8 +690,8 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
     }
     if (K % TBK == 0 && M >= 128 && N >= 128) {
         if (c_i32)
-            return launch_tiled<false, true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
-        return launch_tiled<false, false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+            return launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+        return launch_x32<false, false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
     }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     if (c_i32)

@@ -215,6 +215,7 @@ __global__ void k_fp8_decode(const uint8_t* __restrict__ c, float* __restrict__ 
 
 // ------------------------------------------------------- row / group codecs
 // quantize_int8.c:157-177: one block per row.
+template <bool RNE>
 __global__ void k_quant_int8_rows(const float* __restrict__ x, int8_t* __restrict__ q,
                                   float* __restrict__ scales, size_t rows, size_t cols) {
     __shared__ float sh[16];
@@ -227,7 +228,7 @@ __global__ void k_quant_int8_rows(const float* __restrict__ x, int8_t* __restric
         float inv = 1.0f / s;
         if (threadIdx.x == 0) scales[r] = s;
         for (size_t c = threadIdx.x; c < cols; c += blockDim.x)
-            q[r * cols + c] = (int8_t)clampi(round_i32(xr[c] * inv), -128, 127);
+            q[r * cols + c] = (int8_t)clampi(RNE ? rne_i32(xr[c] * inv) : round_i32(xr[c] * inv), -128, 127);
         __syncthreads();
     }
 }
@@ -642,9 +643,12 @@ int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* st) {
 }
 
 int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
-                          void* st) {
+                          int rne, void* st) {
     int grid = (int)(rows < 65536 ? rows : 65536);
-    k_quant_int8_rows<<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
+    if (rne)
+        k_quant_int8_rows<true><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
+    else
+        k_quant_int8_rows<false><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
     return snx_launch_check("k_quant_int8_rows");
 }
 

@@ -28,7 +28,19 @@ int SNEPPX_dev_quantize_int8_channel(const float* in, int8_t* q, float* scales, 
     REQUIRE(in && q && scales, "dev_quantize_int8_channel: NULL pointer");
     REQUIRE(rows && cols, "dev_quantize_int8_channel: empty matrix");
     snx_clear_error();
-    return snx_k_quant_int8_rows(in, q, scales, rows, cols, stream);
+    return snx_k_quant_int8_rows(in, q, scales, rows, cols, 0, stream);
+}
+
+int SNEPPX_dev_quantize_int8_channel_rounding(const float* in, int8_t* q, float* scales,
+                                              size_t rows, size_t cols, SNEPPXRounding rounding,
+                                              SNEPPXStream stream) {
+    REQUIRE(in && q && scales, "dev_quantize_int8_channel_rounding: NULL pointer");
+    REQUIRE(rows && cols, "dev_quantize_int8_channel_rounding: empty matrix");
+    REQUIRE(rounding == SNEPPX_ROUND_HALF_AWAY || rounding == SNEPPX_ROUND_HALF_EVEN,
+            "dev_quantize_int8_channel_rounding: unknown rounding %d", (int)rounding);
+    snx_clear_error();
+    return snx_k_quant_int8_rows(in, q, scales, rows, cols, rounding == SNEPPX_ROUND_HALF_EVEN,
+                                 stream);
 }
 
 int SNEPPX_dev_quantize_w4_awq(const float* w, uint32_t* qweight, uint16_t* scales,

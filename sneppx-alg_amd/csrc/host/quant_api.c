@@ -160,7 +160,7 @@ int SNEPPX_quantize_int8_channel(const float* input, int8_t* output, size_t rows
     int8_t* dq = arena_take(&a, n);
     float* ds = arena_take(&a, rows * 4);
     TRY(snx_hip_memcpy_h2d(dx, input, n * 4, NULL));
-    TRY(snx_k_quant_int8_rows(dx, dq, ds, rows, cols, NULL));
+    TRY(snx_k_quant_int8_rows(dx, dq, ds, rows, cols, 0, NULL));
     TRY(snx_hip_memcpy_d2h(output, dq, n, NULL));
     TRY(snx_hip_memcpy_d2h(scales_out, ds, rows * 4, NULL));
     TRY(snx_hip_stream_sync(NULL));

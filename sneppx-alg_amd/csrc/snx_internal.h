@@ -53,8 +53,9 @@ int snx_k_fp8_encode(const float* x, uint8_t* c, size_t n, int fmt, const float*
                      void* stream);
 int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* stream);
 
+/* rne: 0 = roundf (the reference), 1 = ties to even */
 int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
-                          void* stream);
+                          int rne, void* stream);
 int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,
                        size_t group, void* stream);
 /* q may be NULL (bits > 8 store no codes); zeros may be NULL */

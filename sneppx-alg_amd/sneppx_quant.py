@@ -65,6 +65,7 @@ EXPORTS = {
     # device entry points
     "SNEPPX_qlinear_last_error": (C.c_char_p, []),
     "SNEPPX_dev_quantize_int8_channel": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_dev_quantize_int8_channel_rounding": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
     "SNEPPX_dev_quantize_w4_awq": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
     "SNEPPX_dev_quantize_w4_gptq": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_fp8_e4m3_scaled": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
@@ -243,10 +244,15 @@ class Library:
             return C.c_void_p(stream)
         return C.c_void_p(torch.cuda.current_stream().cuda_stream)
 
-    def dev_quantize_int8_channel(self, w, q, scales, stream=None):
+    def dev_quantize_int8_channel(self, w, q, scales, stream=None, half_even=False):
         rows, cols = w.shape
-        self.check(self.fn["SNEPPX_dev_quantize_int8_channel"](
-            _ptr(w), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)), "dev_quantize_int8_channel")
+        if half_even:
+            self.check(self.fn["SNEPPX_dev_quantize_int8_channel_rounding"](
+                _ptr(w), _ptr(q), _ptr(scales), rows, cols, 1, self._stream(stream)),
+                "dev_quantize_int8_channel_rounding")
+        else:
+            self.check(self.fn["SNEPPX_dev_quantize_int8_channel"](
+                _ptr(w), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)), "dev_quantize_int8_channel")
 
     def dev_quantize_w4_awq(self, w, qweight, scales, qzeros, group, stream=None):
         N, K = w.shape

@@ -51,6 +51,21 @@ def test_dev_int8_channel_bit_exact(lib, oracle, shape):
     assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [(8, 512), (4096, 4096)])
+def test_dev_int8_channel_half_even_bit_exact(lib, oracle, shape):
+    print(f"[gpu] int8 channel half-even {shape}", flush=True)
+    rng = np.random.default_rng(shape[0])
+    w = rng.normal(0, 0.02, shape).astype(np.float32)
+    w[:4, 0] = 127.0                                       # scale 1: the next values are ties
+    w[:4, 1:5] = np.array([0.5, 1.5, -2.5, 126.5], np.float32)
+    q, s = torch.empty(shape, dtype=torch.int8, device=DEV), torch.empty(shape[0], device=DEV)
+    lib.dev_quantize_int8_channel(to_dev(w), q, s, half_even=True)
+    torch.cuda.synchronize()
+    rc, qo, so = oracle.quantize_int8_channel_rne(w)
+    assert np.array_equal(q.cpu().numpy(), qo) and np.array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+    assert list(q.cpu().numpy()[0, 1:5]) == [0, 2, -2, 126]
+
+
 @pytest.mark.parametrize("N,K,group", [(24, 512, 128), (11008, 4096, 128), (40, 256, 64), (8, 64, 8)])
 def test_dev_w4_awq_bit_exact(lib, oracle, N, K, group):
     print(f"[gpu] w4 awq {N}x{K} g{group}", flush=True)

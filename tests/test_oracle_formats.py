@@ -135,3 +135,27 @@ def test_linears_against_float64(oracle):
     assert np.abs(out - want).max() <= 1e-5 * np.abs(want).max()
     # codes stay below the reference's field-15 (inf/nan) range when |x/s| <= 240
     assert ((ca & 0x78) != 0x78).all() and ((cb & 0x78) != 0x78).all()
+
+
+def test_half_even_option_matches_numpy_rint_and_differs_only_at_ties(oracle):
+    """The build's SNEPPX_ROUND_HALF_EVEN option (C1 config text) against
+    numpy's rint on the same fp32 products; the reference's roundf path
+    differs from it exactly at the odd .5 ties."""
+    rng = np.random.default_rng(17)
+    w = rng.normal(0, 0.02, (64, 512)).astype(np.float32)
+    # plant exact ties: scale is max/127, so max=127 makes x*inv = x
+    w[:8, 0] = 127.0
+    w[:8, 1:9] = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5], np.float32)
+    rc, q_even, s_even = oracle.quantize_int8_channel_rne(w)
+    rc2, q_away, s_away = oracle.quantize_int8_channel(w)
+    assert rc == 0 and rc2 == 0
+    assert np.array_equal(s_even.view(np.uint32), s_away.view(np.uint32))
+    inv = (np.float32(1.0) / s_even).astype(np.float32)
+    prod = (w * inv[:, None]).astype(np.float32)
+    want = np.clip(np.rint(prod), -128, 127).astype(np.int8)
+    assert np.array_equal(q_even, want)
+    assert list(q_even[0, 1:9]) == [0, 2, 2, 0, -2, -2, 126, -126]
+    assert list(q_away[0, 1:9]) == [1, 2, 3, -1, -2, -3, 127, -127]
+    ties = (np.abs(prod - np.trunc(prod)) == 0.5)
+    diff = q_even != q_away
+    assert diff.sum() > 0 and np.all(ties[diff])
