@@ -170,6 +170,22 @@ def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
             "gbs_kernel": nbytes / mean_launch / 1e6, "codes_differing_half_even": mismatch}
 
 
+def bench_host_api(lib, N, K, reps=5):
+    """The reference's host-pointer entry point SNEPPX_quantize_int8_channel
+    (quantize_int8.c:157-177) on the C1 weight: pageable host fp32 in, host
+    int8 codes + scales out, copies over PCIe included (the drop-in path a C
+    caller of quantization.h gets)."""
+    import numpy as np
+    w = np.random.default_rng(11).normal(0, 0.02, (N, K)).astype(np.float32)
+    lib.quantize_int8_channel(w)   # warm-up (first allocation)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        rc, q, s = lib.quantize_int8_channel(w)
+    per = (time.perf_counter() - t0) / reps
+    return {"ms_per_call": per * 1e3, "rc": rc,
+            "gbs_pcie_inclusive": (N * K * 4 + N * K + N * 4) / per / 1e9}
+
+
 def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
     g = torch.Generator(device="cuda").manual_seed(13)
     a32 = torch.randn((M, K), device="cuda", generator=g)
@@ -258,7 +274,9 @@ def bench_chain(lib, timer, torch, steps, warmup):
 
 def cpu_baseline(ws_host, x_host, N, K, group, seconds):
     """The oracle's C restatement (C2 GEMV: dequantise + k-ascending fp32 dot,
-    the reference tensor.c:1820-1823 order), one host thread, -O3."""
+    the reference tensor.c:1820-1823 order), one host thread, -O3.  Also times
+    the restated SNEPPX_quantize_int8_channel on the C1 weight (the host API
+    function the drop-in replaces), for the PCIe-inclusive comparison."""
     import numpy as np
     sys.path.insert(0, os.path.join(REPO, "oracle"))
     from py_oracle import Oracle
@@ -273,9 +291,15 @@ def cpu_baseline(ws_host, x_host, N, K, group, seconds):
             break
     per = el / reps
     nbytes = w4_bytes(1, N, K, K // group)
+    w = np.random.default_rng(11).normal(0, 0.02, (4096, 4096)).astype(np.float32)
+    t1 = time.perf_counter()
+    for _ in range(3):
+        orc.quantize_int8_channel(w)
+    q_ms = (time.perf_counter() - t1) / 3 * 1e3
     return {"value": round(nbytes / per / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"full C2 shape N={N} K={K} M=1, {reps} calls in {el:.1f} s "
                       f"({per * 1e3:.1f} ms/call), oracle/liboracle_perf.so (-O3 -march=x86-64-v3)",
+            "quantize_int8_channel_4096x4096_ms": round(q_ms, 2),
             "host_cpu": _cpu_name(), "host_threads_available": os.cpu_count()}
 
 
@@ -384,6 +408,10 @@ def main():
                       "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                       "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
                       "codes_differing_half_even": r["codes_differing_half_even"]})
+        h = bench_host_api(lib, 4096, 4096)
+        extra.append({"workload": "host API SNEPPX_quantize_int8_channel 4096x4096 (host buffers, PCIe included)",
+                      "value": round(h["ms_per_call"], 3), "unit": "ms", "higher_is_better": False,
+                      "gbs_pcie_inclusive": round(h["gbs_pcie_inclusive"], 2)})
         r = bench_chain(lib, timer, torch, 10, 5)
         extra.append({"workload": f"C5 Llama-3-8B layer W4A16 g128 linear chain T={r['T']} "
                                   f"(16 decode + 8 prefill chunks {r['chunk_lens']})",

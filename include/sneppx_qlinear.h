@@ -59,6 +59,13 @@ int SNEPPX_dev_quantize_int8_channel_rounding(const float* in, int8_t* q, float*
                                               size_t rows, size_t cols, SNEPPXRounding rounding,
                                               SNEPPXStream stream);
 
+/* Device form of SNEPPX_tensor_fake_quant (kernel/tensor/tensor.c:2180-2195,
+ * the QAT forward): out = clamp(floorf(in * (1/scale) + 0.5f), -2^(b-1),
+ * 2^(b-1) - 1) * scale over n floats (in may equal out).  -1 for scale <= 0 or
+ * bits outside [2, 16], as the reference's NULL return. */
+int SNEPPX_dev_fake_quant(const float* in, float* out, size_t n, float scale, int bits,
+                          SNEPPXStream stream);
+
 /* W4 AWQ-style asymmetric uint4 (build-defined, generalises
  * quantize_int8.c:98-123 to 4 bits with a stored fp16 scale):
  * per (row, group): s = fp16((max-min)/15), z = clamp(roundf(-min/s), 0, 15),

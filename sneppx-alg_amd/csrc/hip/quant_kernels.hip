@@ -233,6 +233,20 @@ __global__ void k_quant_int8_rows(const float* __restrict__ x, int8_t* __restric
     }
 }
 
+// tensor.c:2180-2195 (SNEPPX_tensor_fake_quant): q = floorf(x * (1/scale) +
+// 0.5f) clamped to [-2^(b-1), 2^(b-1) - 1], times scale; compiled without
+// contraction, so the multiply and the add round separately as in the oracle.
+__global__ void k_fake_quant(const float* __restrict__ x, float* __restrict__ y, size_t n,
+                             float scale, float inv, float lo, float hi) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float q = floorf(x[i] * inv + 0.5f);
+        if (q < lo) q = lo;
+        if (q > hi) q = hi;
+        y[i] = q * scale;
+    }
+}
+
 // awq.c:135-161: one wave per (row, group).
 __global__ void k_awq_quantize(const float* __restrict__ w, int8_t* __restrict__ q,
                                float* __restrict__ scales, size_t rows, size_t cols, size_t g) {
@@ -650,6 +664,14 @@ int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows,
     else
         k_quant_int8_rows<false><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
     return snx_launch_check("k_quant_int8_rows");
+}
+
+int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* st) {
+    const float lo = (float)(-(1 << (bits - 1))), hi = (float)((1 << (bits - 1)) - 1);
+    const size_t blocks = (n + kBlock - 1) / kBlock;
+    const int grid = (int)(blocks < 65536 ? blocks : 65536);
+    k_fake_quant<<<grid, kBlock, 0, S(st)>>>(x, y, n, scale, 1.0f / scale, lo, hi);
+    return snx_launch_check("k_fake_quant");
 }
 
 int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,

@@ -43,6 +43,16 @@ int SNEPPX_dev_quantize_int8_channel_rounding(const float* in, int8_t* q, float*
                                  stream);
 }
 
+int SNEPPX_dev_fake_quant(const float* in, float* out, size_t n, float scale, int bits,
+                          SNEPPXStream stream) {
+    REQUIRE(in && out, "dev_fake_quant: NULL pointer");
+    REQUIRE(scale > 0.0f, "dev_fake_quant: scale must be > 0");
+    REQUIRE(bits >= 2 && bits <= 16, "dev_fake_quant: bits=%d outside [2, 16]", bits);
+    snx_clear_error();
+    if (n == 0) return 0;
+    return snx_k_fake_quant(in, out, n, scale, bits, stream);
+}
+
 int SNEPPX_dev_quantize_w4_awq(const float* w, uint32_t* qweight, uint16_t* scales,
                                uint32_t* qzeros, size_t N, size_t K, int group,
                                SNEPPXStream stream) {

@@ -56,6 +56,7 @@ int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* stream
 /* rne: 0 = roundf (the reference), 1 = ties to even */
 int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
                           int rne, void* stream);
+int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* stream);
 int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,
                        size_t group, void* stream);
 /* q may be NULL (bits > 8 store no codes); zeros may be NULL */

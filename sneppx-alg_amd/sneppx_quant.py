@@ -66,6 +66,7 @@ EXPORTS = {
     "SNEPPX_qlinear_last_error": (C.c_char_p, []),
     "SNEPPX_dev_quantize_int8_channel": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_int8_channel_rounding": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
+    "SNEPPX_dev_fake_quant": (C.c_int, [_vp, _vp, _sz, C.c_float, C.c_int, _vp]),
     "SNEPPX_dev_quantize_w4_awq": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
     "SNEPPX_dev_quantize_w4_gptq": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_fp8_e4m3_scaled": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
@@ -253,6 +254,10 @@ class Library:
         else:
             self.check(self.fn["SNEPPX_dev_quantize_int8_channel"](
                 _ptr(w), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)), "dev_quantize_int8_channel")
+
+    def dev_fake_quant(self, x, out, scale, bits, stream=None):
+        self.check(self.fn["SNEPPX_dev_fake_quant"](
+            _ptr(x), _ptr(out), x.numel(), scale, bits, self._stream(stream)), "dev_fake_quant")
 
     def dev_quantize_w4_awq(self, w, qweight, scales, qzeros, group, stream=None):
         N, K = w.shape

@@ -406,3 +406,24 @@ def test_silu_mul(lib, T, F):
     got = bf16_to_f32(u16(out)).astype(np.float64)
     # one bf16 rounding of the fp32 value: |err| <= 2^-8 |want| (+ fp32 slack)
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
+
+
+# ---------------------------------------------------------- QAT fake-quant
+@pytest.mark.parametrize("n,scale,bits", [(1, 0.5, 8), (1000, 0.02, 4), (1 << 20, 0.003, 8), (77, 1.0, 16)])
+def test_dev_fake_quant_bit_exact(lib, oracle, n, scale, bits):
+    rng = np.random.default_rng(n + bits)
+    x = rng.normal(0, 1, n).astype(np.float32)
+    x[: min(n, 4)] = np.array([1.4, -0.6, 200.0, np.nan], np.float32)[: min(n, 4)]   # test_fake_quant.c KATs
+    y = torch.empty(n, device=DEV)
+    lib.dev_fake_quant(to_dev(x), y, scale, bits)
+    torch.cuda.synchronize()
+    rc, yo = oracle.fake_quant(x, scale, bits)
+    assert rc == 0
+    assert np.array_equal(y.cpu().numpy().view(np.uint32), yo.view(np.uint32))
+
+
+def test_dev_fake_quant_rejects_bad_arguments(lib):
+    x = torch.zeros(4, device=DEV)
+    for scale, bits in ((0.0, 8), (-1.0, 8), (1.0, 1), (1.0, 17)):
+        with pytest.raises(Exception):
+            lib.dev_fake_quant(x, x, scale, bits)
