@@ -3,19 +3,22 @@
 // y[m][n] = sum_k x[m][k] * (q[n][k] - z[n][g]) * s[n][g],  g = k / group,
 // fp32 accumulation, for large M (prefill / continuous batches).
 //
-//  1. k_w4_prep_x: one pass over the activations writes them in the MFMA
-//     k-slot order the weight unpack produces ({0,4,1,5,2,6,3,7} within every
-//     8 columns) and the fp32 sums X[g128][m] of every 128-column step.
-//  2. k_w4a16_gemm: 128x256 output tiles, 8 waves (2 along M x 4 along N,
-//     64x64 each = 4x4 blocks of v_mfma_f32_16x16x32_bf16), K step 128.
-//     Activation and packed-weight tiles move global->LDS with
-//     global_load_lds_dwordx4 (double-buffered, 2 x 48 KB).  Activation rows
-//     are 256 B; their 16-byte chunks are XOR-swizzled by (row & 15), so the
-//     16 rows of a fragment read 16 different chunks (no bank conflicts).
-//     Weight rows are 64 B and a fragment read covers 1 KB contiguous.
-//     Nibbles become bf16 (128 + q) with one v_and_or_b32 per pair; after each
-//     128-column step the accumulator block is folded into the fp32 result:
-//     y += s * acc - s * (128 + z) * X  (exact bias/zero-point removal).
+//  1. k_w4_prep_x: one pass over the activations writes them in the order
+//     the MFMA operands take them (per 128-column step: 16-byte chunks
+//     permuted, and {0,4,1,5,2,6,3,7} inside a chunk, the order of the nibble
+//     unpack) and the fp32 sums X[t][m] of every 128-column step t.
+//  2. k_w4a16_gemm: 128x256 output tiles, 8 waves side by side along N (each
+//     128 rows x 32 columns = 4 blocks of v_mfma_f32_32x32x16_bf16, which
+//     runs at twice the rate of the 16x16x32 form on gfx950), K step 128.
+//     Activation, packed-weight, scale, zero-point and step-sum slices move
+//     global->LDS with global_load_lds through a three-stage ring; each wave
+//     streams the next-but-one stage in one load per MFMA sub-step.
+//     Activation rows are 256 B with 16-byte chunks XOR-swizzled by
+//     (row & 15); 64-byte weight rows rotate their chunks by bsw(row); both
+//     fragment reads are bank-conflict free.  Nibbles become bf16 (128 + q)
+//     with one v_and_or_b32 per pair; each step folds into the fp32 result as
+//     y += s * acc (VALU) - X * s * (128 + z) (a rank-1 fp32 MFMA), which
+//     removes the bias and zero point exactly.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -29,15 +32,15 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 constexpr int GBM = 128, GBN = 256, GBK = 128;
-constexpr int GFM = 4, GFN = 4;                 // 16x16 blocks per wave along M, N
 constexpr int GLDS_A = GBM * GBK * 2;           // 32 KB of bf16 activations
 constexpr int GLDS_B = GBN * GBK / 2;           // 16 KB of packed weights
-constexpr int GLDS_X = GBM * 4;                 // fp32 step sums of the tile's rows
 
 // ---------------------------------------------------------------- prep pass
 // One thread per 8 columns.  K % 128 == 0, so the 16 threads of one
@@ -58,7 +61,9 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
     p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
     p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
     p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-    if (live) *reinterpret_cast<u32x4*>(xp + itc * 8) = p;
+    // input chunk 8 h + s of its 128-column step goes to chunk 2 s + h
+    const int jin = k8 & 15, jout = 2 * (jin & 7) + (jin >> 3);
+    if (live) *reinterpret_cast<u32x4*>(xp + (itc - jin + jout) * 8) = p;
     float sum = 0.0f;
 #pragma unroll
     for (int e = 0; e < 4; e++)
@@ -71,6 +76,7 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
 }
 
 // ----------------------------------------------------------------- the GEMM
+constexpr int W4_WN = 8;   // waves along N (8 / W4_WN along M)
 // LDS ring of three stages (one K step of 128 columns each):
 //   A   128 rows x 256 B  bf16 activations, chunk c of row r at c ^ (r & 15)
 //   B   256 rows x 64 B   packed weights,   chunk c of row r at c ^ bsw(r)
@@ -79,7 +85,7 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
 //   Z   256 u32           zero-point word of every tile column
 // Every wave issues exactly 8 direct loads per stage, so "stage kt landed"
 // is vmcnt(8) while stage kt + 1 is still in flight.
-constexpr int GOFF_B = GLDS_A, GOFF_X = GOFF_B + GLDS_B, GOFF_S = GOFF_X + GLDS_X;
+constexpr int GOFF_B = GLDS_A, GOFF_X = GOFF_B + GLDS_B, GOFF_S = GOFF_X + GBM * 4;
 constexpr int GOFF_Z = GOFF_S + GBN * 4, GRING = GOFF_Z + GBN * 4;
 constexpr int GSTAGES = 3;
 
@@ -87,7 +93,21 @@ constexpr int GSTAGES = 3;
 // 16-byte chunks rotate by bits 1-3 of the row (conflict-free 16-lane reads)
 __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
-template <bool ZEROS, bool YF32>
+// The MFMAs see weights 128 + q (bf16 of the nibble), so each 128-column
+// step t gives acc_t = sum_k x[m][k] (128 + q[n][k]) and
+//   y[m][n] = sum_t (s_t[n] acc_t[m][n] - X_t[m] c_t[n]),
+//   X_t[m] = sum of x[m][k] over step t,  c_t[n] = s_t[n] (128 + z_t[n]).
+// Per step, s_t acc_t is one VALU FMA per element and the rank-1 term
+// X_t c_t goes to the matrix cores: one v_mfma_f32_32x32x1_f32 (two 32x32
+// outer products) per pair of result blocks, accumulating in fp32.
+//
+// Products use v_mfma_f32_32x32x16_bf16 (operand lane l: row / column l % 32,
+// k = 8 (l / 32) + e; result value v of lane l: row 8 (v / 4) + 4 (l / 32) +
+// v % 4, column l % 32).  Sub-step s of a step takes packed word 8 h + s of
+// each weight column in lanes with h = l / 32, so a lane's eight words for the
+// step are 32 contiguous bytes; the prep pass stores the activations to match
+// (chunk 2 s + h of a prepared row = original columns of word 8 h + s).
+template <bool ZEROS, bool YF32, int WN>
 __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
                                                     const float* __restrict__ xs,
                                                     const uint32_t* __restrict__ qw,
@@ -95,11 +115,17 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                                                     const uint32_t* __restrict__ qz,
                                                     void* __restrict__ y, int M, int N, int K,
                                                     int G, int gshift, int Mp, int tiles_m) {
+    // WN waves along N, 8 / WN along M: each wave owns RW rows x CW columns,
+    // FM x FN blocks of 32 x 32; the result sits in FM / 2 x FN pairs of
+    // blocks stacked along M (the 2-block f32 MFMA's output)
+    constexpr int WM = 8 / WN, RW = GBM / WM, CW = GBN / WN, FM = RW / 32, FN = CW / 32;
+    constexpr int QM = FM / 2;
+    static_assert(FM % 2 == 0 && FN >= 1, "wave tile must hold pairs of 32-row blocks");
     extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 2, wn = wave & 3;
-    const int r16 = lane & 15, q = lane >> 4;
+    const int wm = wave / WN, wn = wave % WN;
+    const int r32 = lane & 31, h = lane >> 5;
 
     // XCD-aware order: consecutive tiles of one M-row of tiles share an XCD
     const int b = blockIdx.x, nb = gridDim.x;
@@ -136,68 +162,77 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     const int zw = (G + 7) >> 3;
     const uint8_t* xpb = reinterpret_cast<const uint8_t*>(xp);
     const uint8_t* qwb = reinterpret_cast<const uint8_t*>(qw);
-    auto dload = [&](int buf, int kt) {
+    // load p (0..7) of the eight each wave issues for stage kt into ring slot buf
+    auto dpart = [&](int buf, int kt, int p) {
         uint8_t* base = lds + buf * GRING;
-        const uint32_t ka = (uint32_t)kt * (GBK * 2), kw = (uint32_t)kt * (GBK / 2);
-        const int g = (kt * GBK) >> gshift;
+        if (p < 4) {
+            __builtin_amdgcn_global_load_lds(xpb + (ga[p] + (uint32_t)kt * (GBK * 2)),
+                                             base + (8 * p + wave) * 1024, 16, 0, 0);
+        } else if (p < 6) {
+            __builtin_amdgcn_global_load_lds(qwb + (gw[p - 4] + (uint32_t)kt * (GBK / 2)),
+                                             base + GOFF_B + (8 * (p - 4) + wave) * 1024, 16, 0, 0);
+        } else if (p == 6) {
+            const int g = (kt * GBK) >> gshift;
+            if (zload)
+                __builtin_amdgcn_global_load_lds(qz + (size_t)sn * zw + (g >> 3),
+                                                 base + GOFF_Z + 256 * (wave & 3), 4, 0, 0);
+            else
+                __builtin_amdgcn_global_load_lds(scales + (size_t)sn * G + (g & ~1),
+                                                 base + GOFF_S + 256 * (wave & 3), 4, 0, 0);
+        } else {
+            // step sums of the tile's 128 rows (each half loaded by four waves)
+            __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + (wave & 1) * 64 + lane,
+                                             base + GOFF_X + (wave & 1) * 256, 4, 0, 0);
+        }
+    };
+    auto dload = [&](int buf, int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds(xpb + (ga[i] + ka), base + (8 * i + wave) * 1024, 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            __builtin_amdgcn_global_load_lds(qwb + (gw[i] + kw), base + GOFF_B + (8 * i + wave) * 1024, 16, 0, 0);
-        if (zload)
-            __builtin_amdgcn_global_load_lds(qz + (size_t)sn * zw + (g >> 3),
-                                             base + GOFF_Z + 256 * (wave & 3), 4, 0, 0);
-        else
-            __builtin_amdgcn_global_load_lds(scales + (size_t)sn * G + (g & ~1),
-                                             base + GOFF_S + 256 * (wave & 3), 4, 0, 0);
-        // step sums of the tile's 128 rows (each half loaded by four waves)
-        __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + (wave & 1) * 64 + lane,
-                                         base + GOFF_X + (wave & 1) * 256, 4, 0, 0);
+        for (int p = 0; p < 8; p++) dpart(buf, kt, p);
     };
 
-    f32x4 yacc[GFM][GFN];
+    f32x32 yq[QM][FN];
 #pragma unroll
-    for (int i = 0; i < GFM; i++)
+    for (int i = 0; i < QM; i++)
 #pragma unroll
-        for (int j = 0; j < GFN; j++) yacc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < FN; j++) yq[i][j] = f32x32{};
 
     uint32_t nib_mask, bf_bias;
     asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
 
     const int nk = K / GBK;
-    const int mrow = m0 + wm * 64 + q * 4;       // + 16 i + e
-    const uint8_t* arow = lds + (wm * 64 + r16) * (GBK * 2);
-    const uint8_t* wrow = lds + GOFF_B + (wn * 64 + r16) * (GBK / 2) + ((q ^ bsw(r16)) << 4);
+    // activation fragment: row wm RW + 32 i + r32, logical chunk 2 s + h
+    // (rows 16 apart share the swizzle, so row & 15 = r32 & 15)
+    const uint8_t* arow = lds + (wm * RW + r32) * (GBK * 2);
+    // weight words 8 h .. 8 h + 7 of column wn CW + 32 j + r32 = chunks 2 h, 2 h + 1
+    const int brow = wn * CW + r32;
+    const uint8_t* wrow0 = lds + GOFF_B + brow * (GBK / 2) + (((2 * h) ^ bsw(brow)) << 4);
+    const uint8_t* wrow1 = lds + GOFF_B + brow * (GBK / 2) + (((2 * h + 1) ^ bsw(brow)) << 4);
 
-    // fold one 128-column step into the result: y += s*acc - s*(128+z)*X
-    auto fold = [&](const f32x4 (&acc)[GFM][GFN], const f32x4* xr, const uint32_t* sr,
+    // fold one 128-column step into the result: y += s * acc - X (s (128 + z))
+    auto fold = [&](const f32x16 (&acc)[FM][FN], const float* xr, const uint32_t* sr,
                     const uint32_t* zr, int g) {
 #pragma unroll
-        for (int j = 0; j < GFN; j++) {
-            const uint16_t h = (uint16_t)(sr[j] >> (16 * (g & 1)));
-            const float sf = (float)__builtin_bit_cast(_Float16, h);
+        for (int j = 0; j < FN; j++) {
+            const uint16_t hs = (uint16_t)(sr[j] >> (16 * (g & 1)));
+            const float sf = (float)__builtin_bit_cast(_Float16, hs);
             const uint32_t z = ZEROS ? (zr[j] >> (4 * (g & 7))) & 15u : 8u;
             const float nc = -sf * (float)(128u + z);
 #pragma unroll
-            for (int i = 0; i < GFM; i++)
+            for (int i = 0; i < QM; i++) {
+                yq[i][j] = __builtin_amdgcn_mfma_f32_32x32x1f32(xr[i], nc, yq[i][j], 0, 0, 0);
 #pragma unroll
-                for (int e = 0; e < 4; e++)
-                    yacc[i][j][e] = __builtin_fmaf(nc, xr[i][e], __builtin_fmaf(sf, acc[i][j][e], yacc[i][j][e]));
+                for (int u = 0; u < 2; u++)
+#pragma unroll
+                    for (int e = 0; e < 16; e++)
+                        yq[i][j][16 * u + e] = __builtin_fmaf(sf, acc[2 * i + u][j][e], yq[i][j][16 * u + e]);
+            }
         }
     };
 
-    // The two waves that share a SIMD (w and w + 4) run half a step apart:
-    // waves 4..7 fold a step after the next barrier, while waves 0..3 issue
-    // that step's MFMAs, and the other way round at the end of the step, so
-    // the fp32 fold of one wave overlaps the MFMAs of the other.
-    const bool late = wave >= 4;
-    uint32_t sr[GFN], zr[GFN];
-    f32x4 xr[GFM];
-    f32x4 acc[GFM][GFN];
-    int gp = 0;
+    uint32_t sr[FN], zr[FN];
+    float xr[QM];
+    f32x16 acc[FM][FN];
     dload(0, 0);
     dload(1, nk > 1 ? 1 : 0);
     for (int kt = 0; kt < nk; kt++) {
@@ -206,23 +241,25 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
         __syncthreads();                      // and every wave is done with stage kt - 1
         __builtin_amdgcn_sched_barrier(0);    // nothing below moves above the wait
         const int kn = kt + 2 < nk ? kt + 2 : nk - 1;   // past the end: reload, unused
-        dload((kt + 2) % GSTAGES, kn);
-        if (late && kt > 0) fold(acc, xr, sr, zr, gp);
+        const int nbuf = (kt + 2) % GSTAGES;
 
         const uint8_t* ab = arow + cur * GRING;
-        const uint8_t* wb = wrow + cur * GRING;
-        u32x4 wv[GFN];
+        u32x4 wv[FN][2];
 #pragma unroll
-        for (int j = 0; j < GFN; j++) wv[j] = *reinterpret_cast<const u32x4*>(wb + j * 16 * (GBK / 2));
+        for (int j = 0; j < FN; j++) {
+            wv[j][0] = *reinterpret_cast<const u32x4*>(wrow0 + cur * GRING + j * 32 * (GBK / 2));
+            wv[j][1] = *reinterpret_cast<const u32x4*>(wrow1 + cur * GRING + j * 32 * (GBK / 2));
+        }
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
-            bf16x8 fa[GFM], fb[GFN];
+        for (int s = 0; s < 8; s++) {
+            bf16x8 fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < GFM; i++)
-                fa[i] = *reinterpret_cast<const bf16x8*>(ab + i * 16 * (GBK * 2) + (((4 * q + s) ^ r16) << 4));
+            for (int i = 0; i < FM; i++)
+                fa[i] = *reinterpret_cast<const bf16x8*>(ab + i * 32 * (GBK * 2) +
+                                                          (((2 * s + h) ^ (r32 & 15)) << 4));
 #pragma unroll
-            for (int j = 0; j < GFN; j++) {
-                const uint32_t w = wv[j][s];
+            for (int j = 0; j < FN; j++) {
+                const uint32_t w = wv[j][s >> 2][s & 3];
                 u32x4 bq;
                 bq[0] = (w & nib_mask) | bf_bias;
                 bq[1] = ((w >> 4) & nib_mask) | bf_bias;
@@ -231,53 +268,54 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                 fb[j] = __builtin_bit_cast(bf16x8, bq);
             }
 #pragma unroll
-            for (int i = 0; i < GFM; i++)
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < GFN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        fa[i], fb[j], s == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : acc[i][j], 0, 0, 0);
+                for (int j = 0; j < FN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                        fa[i], fb[j], s == 0 ? f32x16{} : acc[i][j], 0, 0, 0);
+            // stage kt + 2 streams in one load per sub-step, between the MFMAs
+            dpart(nbuf, kn, s);
         }
-        // this step's sums, scales and zero words (the ring slot is refilled
-        // after the next barrier, so the late waves keep them in registers)
+        // this step's sums, scales and zero words; the 2-block f32 MFMA takes
+        // row 64 i + lane of the wave's rows
         const uint8_t* st = lds + cur * GRING;
-        const float* xb = reinterpret_cast<const float*>(st + GOFF_X) + wm * 64 + q * 4;
 #pragma unroll
-        for (int i = 0; i < GFM; i++) xr[i] = *reinterpret_cast<const f32x4*>(xb + i * 16);
+        for (int i = 0; i < QM; i++)
+            xr[i] = reinterpret_cast<const float*>(st + GOFF_X)[wm * RW + 64 * i + lane];
 #pragma unroll
-        for (int j = 0; j < GFN; j++) {
-            const int c = wn * 64 + j * 16 + r16;
+        for (int j = 0; j < FN; j++) {
+            const int c = wn * CW + j * 32 + r32;
             sr[j] = reinterpret_cast<const uint32_t*>(st + GOFF_S)[c];
             zr[j] = ZEROS ? reinterpret_cast<const uint32_t*>(st + GOFF_Z)[c] : 0u;
         }
-        const int g = (kt * GBK) >> gshift;
-        if (!late)
-            fold(acc, xr, sr, zr, g);
-        else
-            gp = g;
+        fold(acc, xr, sr, zr, (kt * GBK) >> gshift);
     }
-    if (late) fold(acc, xr, sr, zr, gp);
     __builtin_amdgcn_s_waitcnt(0x0070);   // the ring's last (unused) loads drain before exit
 
+    // value 16 u + v of pair (i, j), lane l: block (2 i + u, j), row
+    // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
 #pragma unroll
-    for (int i = 0; i < GFM; i++) {
+    for (int i = 0; i < QM; i++) {
 #pragma unroll
-        for (int j = 0; j < GFN; j++) {
-            const int n = n0 + wn * 64 + j * 16 + r16;
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + wn * CW + j * 32 + r32;
             if (n >= N) continue;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = mrow + i * 16 + e;
-                if (m >= M) continue;
-                if (YF32)
-                    reinterpret_cast<float*>(y)[(size_t)m * N + n] = yacc[i][j][e];
-                else
-                    reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = bf16_out(yacc[i][j][e]);
-            }
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int m = m0 + wm * RW + 32 * (2 * i + u) + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (m >= M) continue;
+                    if (YF32)
+                        reinterpret_cast<float*>(y)[(size_t)m * N + n] = yq[i][j][16 * u + v];
+                    else
+                        reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = bf16_out(yq[i][j][16 * u + v]);
+                }
         }
     }
 }
 
-template <bool ZEROS, bool YF32>
+template <bool ZEROS, bool YF32, int WN>
 int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                    const uint16_t* scales, const uint32_t* qz, void* y, int M, int N, int K,
                    int group, int Mp, hipStream_t st) {
@@ -285,7 +323,7 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
     const size_t lds = (size_t)GSTAGES * GRING;
     static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
             snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
             return -1;
@@ -293,7 +331,7 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
         attr_set = true;
     }
     const int gshift = __builtin_ctz((unsigned)group);
-    k_w4a16_gemm<ZEROS, YF32><<<tiles_m * tiles_n, 512, lds, st>>>(
+    k_w4a16_gemm<ZEROS, YF32, WN><<<tiles_m * tiles_n, 512, lds, st>>>(
         xp, xs, qw, scales, qz, y, M, N, K, K / group, gshift, Mp, tiles_m);
     return snx_launch_check("k_w4a16_gemm");
 }
@@ -354,11 +392,11 @@ int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
     const int m = (int)M, n = (int)N, k = (int)K, mp = (int)Mp;
     if (qzeros) {
-        if (y_f32) return launch_w4_gemm<true, true>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
-        return launch_w4_gemm<true, false>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+        if (y_f32) return launch_w4_gemm<true, true, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+        return launch_w4_gemm<true, false, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
     }
-    if (y_f32) return launch_w4_gemm<false, true>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
-    return launch_w4_gemm<false, false>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+    if (y_f32) return launch_w4_gemm<false, true, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+    return launch_w4_gemm<false, false, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
 }
 
 }  // extern "C"
