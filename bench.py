@@ -213,6 +213,40 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
             "tops_kernel": ops / mean_launch / 1e9}
 
 
+def bench_vendor_w8a8(torch, M, N, K, steps, warmup):
+    """The same C4 shape through the vendor GEMM library (hipBLASLt behind
+    torch._int_mm / torch._scaled_mm), timed the same way: a reference point
+    for what the hardware delivers on this shape, not part of this library."""
+    out = []
+    g = torch.Generator(device="cuda").manual_seed(17)
+    a = torch.randint(-127, 128, (M, K), device="cuda", dtype=torch.int8, generator=g)
+    w = torch.randint(-127, 128, (N, K), device="cuda", dtype=torch.int8, generator=g)
+    af = (torch.randn((M, K), device="cuda", generator=g)).to(torch.float8_e4m3fn)
+    wf = (torch.randn((N, K), device="cuda", generator=g)).to(torch.float8_e4m3fn)
+    one = torch.ones((), device="cuda")
+    cases = [("int8 torch._int_mm", lambda: torch._int_mm(a, w.t())),
+             ("fp8 e4m3 torch._scaled_mm", lambda: torch._scaled_mm(af, wf.t(), scale_a=one, scale_b=one,
+                                                                    out_dtype=torch.bfloat16))]
+    for name, f in cases:
+        try:
+            for _ in range(warmup):
+                f()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                f()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / steps
+            out.append({"workload": f"vendor reference (hipBLASLt, not this library): {name} M={M} N={N} K={K}",
+                        "value": round(2 * M * N * K / ms / 1e9, 1), "unit": "TOPS", "ms_per_step": round(ms, 4)})
+        except Exception as e:   # a torch build without the op: report, do not fail the bench
+            out.append({"workload": f"vendor reference: {name}", "value": None, "error": str(e)[:120]})
+    del a, w, af, wf
+    return out
+
+
 def llama_tokens(seed=5):
     """C5 ragged continuous batch: 16 decode rows + 8 prefill chunks of
     lengths uniform in [32, 512] (seeded), packed into one token matrix."""
@@ -428,6 +462,7 @@ def main():
                           "value": round(r["tops"], 1), "unit": "TOPS",
                           "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4)})
         torch.cuda.synchronize()
+        extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, 50, 30))
 
     cpu = None
     if not args.no_cpu:
