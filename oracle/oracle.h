@@ -89,6 +89,9 @@ int orc_cholesky_inv(float* h, size_t dim);
 int orc_quant_params_create(orc_quant_params* p, int mode);
 const char* orc_quant_mode_name(int mode);
 
+/* weights.c:225-252 model-zoo int8 (multiplier 127/max, truncation) */
+int orc_quantize_int8_modelzoo(const float* in, int8_t* out, size_t n, float* mult_out);
+
 /* tensor.c:2180-2195 forward rule; returns -1 where the reference returns NULL */
 int orc_fake_quant(const float* in, float* out, size_t n, float scale, int bits);
 

@@ -548,6 +548,30 @@ int orc_fake_quant(const float* in, float* out, size_t n, float scale, int bits)
     return 0;
 }
 
+/* algorithms/model_zoo/weights.c:225-252 (weight_tensor_quantize_int8): one
+ * multiplier for the tensor, codes by truncation toward zero.  The
+ * reference's (int8_t) cast of NaN is undefined in C; on x86-64 gcc emits
+ * cvttss2si, whose NaN result 0x80000000 narrows to 0, which is what this
+ * states explicitly. */
+int orc_quantize_int8_modelzoo(const float* in, int8_t* out, size_t n, float* mult_out)
+{
+    if (!in || !out || !mult_out || n == 0) return -1;
+    float max_val = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float v = fabsf(in[i]);
+        if (v > max_val) max_val = v;
+    }
+    float scale = max_val > 0 ? 127.0f / max_val : 1.0f;
+    for (size_t i = 0; i < n; i++) {
+        float v = in[i] * scale;
+        if (v > 127) v = 127;
+        else if (v < -128) v = -128;
+        out[i] = v != v ? 0 : (int8_t)v;
+    }
+    *mult_out = scale;
+    return 0;
+}
+
 /* tensor.c:1820-1823 (i, j outer; l inner, sequential fp32 from 0.0f) */
 void orc_matmul_kn(const float* a, const float* b, float* y, size_t M, size_t K, size_t N)
 {

@@ -74,6 +74,7 @@ _ORACLE_ONLY = {
     "quantize_int8_channel_rne": (C.c_int, [_f32p, _i8p, _sz, _sz, _f32p]),
     "gptq_quantize_literal": _COMMON["gptq_quantize"],
     "fake_quant": (C.c_int, [_f32p, _f32p, _sz, C.c_float, C.c_int]),
+    "quantize_int8_modelzoo": (C.c_int, [_f32p, _i8p, _sz, C.POINTER(C.c_float)]),
     "matmul_kn": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz]),
     "matmul_nk": (None, [_f32p, _f32p, _f32p, _sz, _sz, _sz]),
     "f32_to_bf16": (C.c_uint16, [C.c_float]),
@@ -248,6 +249,13 @@ class Oracle(_Lib):
         rc = self.raw["fake_quant"](x, y, x.size, scale, bits)
         return rc, y
 
+    def quantize_int8_modelzoo(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        q = np.zeros(x.size, np.int8)
+        m = C.c_float(0)
+        rc = self.raw["quantize_int8_modelzoo"](x, q, x.size, C.byref(m))
+        return rc, q, np.float32(m.value)
+
     def matmul_nk(self, a, w):
         a = np.ascontiguousarray(a, np.float32)
         w = np.ascontiguousarray(w, np.float32)
@@ -358,11 +366,46 @@ class Oracle(_Lib):
         return out
 
 
+class _WeightTensor(C.Structure):
+    """WeightTensor (include/neural_core/model_zoo/weights.h:39-48)."""
+    _fields_ = [("name", C.c_char_p), ("shape", C.POINTER(C.c_int64)), ("ndim", C.c_int),
+                ("numel", C.c_size_t), ("dtype", C.c_void_p), ("data", C.c_void_p),
+                ("data_size", C.c_size_t), ("owns_data", C.c_int)]
+
+
 class Reference(_Lib):
-    """The reference's kernel/quantization sources compiled unchanged (build container only)."""
+    """The reference's kernel/quantization sources and model_zoo/weights.c
+    compiled unchanged (build container only)."""
 
     def __init__(self):
         super().__init__(REF_SO, "SNEPPX_", _COMMON)
+
+    def modelzoo_quantize_int8(self, x):
+        """weight_tensor_quantize_int8 (weights.c:225-252) on a float32 vector:
+        the tensor's buffers are malloc'd by libc because the function frees
+        and replaces them; returns (rc, int8 codes)."""
+        libc = C.CDLL(None)
+        libc.malloc.restype = C.c_void_p
+        libc.malloc.argtypes = [C.c_size_t]
+        libc.free.argtypes = [C.c_void_p]
+        libc.strdup.restype = C.c_void_p
+        libc.strdup.argtypes = [C.c_char_p]
+        f = self.lib.weight_tensor_quantize_int8
+        f.restype, f.argtypes = C.c_int, [C.POINTER(_WeightTensor)]
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        t = _WeightTensor()
+        t.numel = x.size
+        t.data = libc.malloc(max(x.nbytes, 1))
+        C.memmove(t.data, x.ctypes.data, x.nbytes)
+        t.data_size = x.nbytes
+        t.dtype = libc.strdup(b"float32")
+        rc = f(C.byref(t))
+        q = np.zeros(x.size, np.int8)
+        if rc == 0:
+            C.memmove(q.ctypes.data, t.data, x.size)
+        libc.free(t.data)
+        libc.free(t.dtype)
+        return rc, q
 
 
 def reference_available() -> bool:

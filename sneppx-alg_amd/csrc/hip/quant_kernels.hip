@@ -123,6 +123,19 @@ __global__ void k_finalize(const float* __restrict__ part, int nparts, int kind,
     float m = 0.0f;
     for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = nanless_max(m, part[i]);
     m = block_reduce(m, nanless_max, sh);
+    if (kind == SNX_SCALE_MODELZOO) {
+        // weights.c:233-240: the scan ignores NaN (a false compare); the
+        // multiplier is 127 / max, or 1 for an all-zero tensor
+        if (threadIdx.x == 0) {
+            const float mult = m > 0.0f ? 127.0f / m : 1.0f;
+            rec[0] = mult;
+            rec[1] = 1.0f / mult;
+            rec[2] = 0.0f;
+            rec[3] = 0.0f;
+            if (scale_out) scale_out[0] = mult;
+        }
+        return;
+    }
     if (threadIdx.x == 0) {
         float div = kind == SNX_SCALE_SYM127 ? 127.0f : kind == SNX_SCALE_SYM7 ? 7.0f : 240.0f;
         bool degenerate = m < FLT_MIN;
@@ -143,6 +156,20 @@ __global__ void k_quant_int8_sym(const float* __restrict__ x, int8_t* __restrict
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x)
         q[i] = zero ? 0 : (int8_t)clampi(round_i32(x[i] * inv), -128, 127);
+}
+
+// weights.c:242-247: v = x * m clamped to [-128, 127], converted by
+// truncation toward zero; the x86 conversion of NaN gives 0, so does this one.
+__global__ void k_quant_int8_modelzoo(const float* __restrict__ x, int8_t* __restrict__ q,
+                                      size_t n, const float* __restrict__ rec) {
+    const float mult = rec[0];
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = x[i] * mult;
+        if (v > 127.0f) v = 127.0f;
+        else if (v < -128.0f) v = -128.0f;
+        q[i] = v != v ? (int8_t)0 : (int8_t)(int)v;
+    }
 }
 
 __global__ void k_dequant_int8_sym(const int8_t* __restrict__ q, float* __restrict__ y, size_t n,
@@ -611,6 +638,11 @@ int snx_k_finalize_scale(const float* part, int nparts, int kind, const float* x
 int snx_k_quant_int8_sym(const float* x, int8_t* q, size_t n, const float* rec, void* st) {
     k_quant_int8_sym<<<grid_for(n, kBlock * 4), kBlock, 0, S(st)>>>(x, q, n, rec);
     return snx_launch_check("k_quant_int8_sym");
+}
+
+int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec, void* st) {
+    k_quant_int8_modelzoo<<<grid_for(n, kBlock * 4), kBlock, 0, S(st)>>>(x, q, n, rec);
+    return snx_launch_check("k_quant_int8_modelzoo");
 }
 
 int snx_k_dequant_int8_sym(const int8_t* q, float* y, size_t n, float scale, void* st) {

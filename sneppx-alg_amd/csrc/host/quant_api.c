@@ -14,6 +14,7 @@
 
 #include "sneppx_quantization.h"
 #include "sneppx_qlinear.h"
+#include "sneppx_qstore.h"
 #include "snx_hip.h"
 #include "../snx_internal.h"
 
@@ -426,4 +427,51 @@ const char* SNEPPX_quant_mode_name(SNEPPXQuantMode mode) {
     static const char* const names[] = {"none", "int8_sym", "int8_asym", "int4_sym",
                                         "fp8_e4m3", "fp8_e5m2", "awq", "gptq"};
     return ((int)mode >= 0 && (int)mode < 8) ? names[mode] : "unknown";
+}
+
+/* algorithms/model_zoo/weights.c:225-252 (weight_tensor_quantize_int8) */
+int SNEPPX_quantize_int8_modelzoo(const float* input, int8_t* output, size_t n,
+                                  float* multiplier_out) {
+    if (!input || !output || !multiplier_out || n == 0) return -1;
+    int rc = -1;
+    float rec[SNX_SCALE_REC];
+    arena a;
+    if (arena_open(&a, pad(n * 4) + pad(n) + pad(parts_bytes(n)) + pad(16))) return -1;
+    float* dx = arena_take(&a, n * 4);
+    int8_t* dq = arena_take(&a, n);
+    float* dpart = arena_take(&a, parts_bytes(n));
+    float* drec = arena_take(&a, 16);
+    TRY(snx_hip_memcpy_h2d(dx, input, n * 4, NULL));
+    TRY(scale_record(dx, n, SNX_SCALE_MODELZOO, dpart, drec));
+    TRY(snx_k_quant_int8_modelzoo(dx, dq, n, drec, NULL));
+    TRY(snx_hip_memcpy_d2h(output, dq, n, NULL));
+    TRY(snx_hip_memcpy_d2h(rec, drec, sizeof rec, NULL));
+    TRY(snx_hip_stream_sync(NULL));
+    *multiplier_out = rec[0];
+    rc = 0;
+out:
+    arena_close(&a);
+    return rc;
+}
+
+int SNEPPX_dev_quantize_int8_modelzoo(const float* in, int8_t* q, float* d_multiplier_out,
+                                      size_t n, SNEPPXStream stream) {
+    if (!in || !q || !d_multiplier_out) {
+        snx_set_error("dev_quantize_int8_modelzoo: NULL pointer");
+        return -1;
+    }
+    if (n == 0) {
+        snx_set_error("dev_quantize_int8_modelzoo: empty tensor");
+        return -1;
+    }
+    snx_clear_error();
+    const int parts = snx_reduce_parts(n);
+    /* partial maxima and the scale record in the stream's workspace */
+    float* ws = (float*)snx_workspace(((size_t)parts * 2 + SNX_SCALE_REC) * sizeof(float), 0, stream);
+    if (!ws) return -1;
+    float* rec = ws + (size_t)parts * 2;
+    if (snx_k_absmax(in, n, ws, parts, stream)) return -1;
+    if (snx_k_finalize_scale(ws, parts, SNX_SCALE_MODELZOO, in, rec, d_multiplier_out, stream))
+        return -1;
+    return snx_k_quant_int8_modelzoo(in, q, n, rec, stream);
 }

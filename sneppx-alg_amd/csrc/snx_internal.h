@@ -26,7 +26,8 @@ enum {
     SNX_SCALE_SYM127 = 0,   /* int8 sym: max/127 (quantize_int8.c:52-59) */
     SNX_SCALE_SYM7 = 1,     /* int4 sym: max/7   (quantize_int8.c:198-205) */
     SNX_SCALE_ASYM255 = 2,  /* int8 asym: (max-min)/255, zp (quantize_int8.c:102-117) */
-    SNX_SCALE_FP8_240 = 3   /* per-tensor fp8: max/240 (build-defined) */
+    SNX_SCALE_FP8_240 = 3,  /* per-tensor fp8: max/240 (build-defined) */
+    SNX_SCALE_MODELZOO = 4  /* model-zoo int8 multiplier 127/max (weights.c:233-240) */
 };
 
 /* Scale record written by snx_k_finalize_scale (device memory, 4 floats):
@@ -56,6 +57,9 @@ int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* stream
 /* rne: 0 = roundf (the reference), 1 = ties to even */
 int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
                           int rne, void* stream);
+/* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
+int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,
+                              void* stream);
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* stream);
 int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,
                        size_t group, void* stream);

@@ -80,6 +80,33 @@ EXPORTS = {
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    # quantized weights on disk + model-zoo int8 (include/sneppx_qstore.h)
+    "SNEPPX_qstore_open": (_vp, [C.c_char_p]),
+    "SNEPPX_qstore_close": (None, [_vp]),
+    "SNEPPX_qstore_count": (_sz, [_vp]),
+    "SNEPPX_qstore_name": (C.c_char_p, [_vp, _sz]),
+    "SNEPPX_qstore_info": (C.c_int, [_vp, C.c_char_p, C.POINTER(C.c_int), C.POINTER(_sz),
+                                     C.POINTER(_sz), C.POINTER(_sz)]),
+    "SNEPPX_qstore_data": (_vp, [_vp, C.c_char_p, C.POINTER(_sz)]),
+    "SNEPPX_qstore_read_device": (C.c_int, [_vp, C.c_char_p, _vp, _sz, _vp]),
+    "SNEPPX_qstore_metadata": (C.c_char_p, [_vp, C.c_char_p]),
+    "SNEPPX_qstore_writer_open": (_vp, [C.c_char_p]),
+    "SNEPPX_qstore_writer_add_host": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(_sz), _sz, _vp]),
+    "SNEPPX_qstore_writer_add_device": (C.c_int, [_vp, C.c_char_p, C.c_int, C.POINTER(_sz), _sz, _vp,
+                                                  _vp]),
+    "SNEPPX_qstore_writer_set_metadata": (C.c_int, [_vp, C.c_char_p, C.c_char_p]),
+    "SNEPPX_qstore_writer_close": (C.c_int, [_vp]),
+    "SNEPPX_qstore_save_w4": (C.c_int, [_vp, C.c_char_p, _vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _sz,
+                                        _vp]),
+    "SNEPPX_qstore_query_w4": (C.c_int, [_vp, C.c_char_p, C.POINTER(_sz), C.POINTER(_sz),
+                                         C.POINTER(_sz), C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                         C.POINTER(C.c_int)]),
+    "SNEPPX_qstore_load_w4": (C.c_int, [_vp, C.c_char_p, _vp, _vp, _vp, _vp, _vp]),
+    "SNEPPX_qstore_save_w8": (C.c_int, [_vp, C.c_char_p, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_qstore_query_w8": (C.c_int, [_vp, C.c_char_p, C.POINTER(_sz), C.POINTER(_sz)]),
+    "SNEPPX_qstore_load_w8": (C.c_int, [_vp, C.c_char_p, _vp, _vp, _vp]),
+    "SNEPPX_quantize_int8_modelzoo": (C.c_int, [_f32p, _i8p, _sz, C.POINTER(C.c_float)]),
+    "SNEPPX_dev_quantize_int8_modelzoo": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
@@ -326,6 +353,31 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w8a8_fp8"](
             _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), M, N, K, self._stream(stream)), "qlinear_w8a8_fp8")
 
+    # ---------------- model-zoo int8 (weights.c:225-252) -------------------
+    def quantize_int8_modelzoo(self, x):
+        x = np.ascontiguousarray(x, np.float32).ravel()
+        q = np.zeros(x.size, np.int8)
+        m = C.c_float(0)
+        rc = self.fn["SNEPPX_quantize_int8_modelzoo"](x, q, x.size, C.byref(m))
+        return rc, q, np.float32(m.value)
+
+    def dev_quantize_int8_modelzoo(self, x, q, mult, stream=None):
+        self.check(self.fn["SNEPPX_dev_quantize_int8_modelzoo"](
+            _ptr(x), _ptr(q), _ptr(mult), x.numel(), self._stream(stream)), "dev_quantize_int8_modelzoo")
+
+    # ---------------- quantized weights on disk (safetensors) --------------
+    def qstore_open(self, path):
+        h = self.fn["SNEPPX_qstore_open"](os.fsencode(path))
+        if not h:
+            raise SneppxError(f"qstore_open failed: {self.last_error()}")
+        return QStore(self, h)
+
+    def qstore_writer(self, path):
+        h = self.fn["SNEPPX_qstore_writer_open"](os.fsencode(path))
+        if not h:
+            raise SneppxError(f"qstore_writer_open failed: {self.last_error()}")
+        return QStoreWriter(self, h)
+
     # ---------------- HIP events on an explicit stream ----------------------
     def event(self):
         e = C.c_void_p()
@@ -346,6 +398,131 @@ class Library:
         cu, clk = C.c_int(0), C.c_int(0)
         self.check(self.fn["snx_hip_device_info"](buf, 128, C.byref(cu), C.byref(clk)), "device_info")
         return buf.value.decode(), cu.value, clk.value
+
+
+# dtype codes of include/sneppx_qstore.h (= the reference's SNEPPXSafetensorsDType)
+QST_DTYPES = ["F32", "F16", "F64", "I64", "I32", "I16", "I8", "U8", "BOOL", "BF16", "F8_E5M2",
+              "F8_E4M3FN"]
+QST_NUMPY = {"F32": np.float32, "F16": np.float16, "F64": np.float64, "I64": np.int64,
+             "I32": np.int32, "I16": np.int16, "I8": np.int8, "U8": np.uint8, "BOOL": np.bool_,
+             "BF16": np.uint16, "F8_E5M2": np.uint8, "F8_E4M3FN": np.uint8}
+
+
+def _shape_arg(shape):
+    return (_sz * max(len(shape), 1))(*shape), len(shape)
+
+
+class QStore:
+    """A safetensors file opened by SNEPPX_qstore_open (read-only mapping)."""
+
+    def __init__(self, lib, handle):
+        self.L, self.h = lib, C.c_void_p(handle)
+
+    def close(self):
+        if self.h:
+            self.L.fn["SNEPPX_qstore_close"](self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def names(self):
+        n = self.L.fn["SNEPPX_qstore_count"](self.h)
+        return [self.L.fn["SNEPPX_qstore_name"](self.h, i).decode() for i in range(n)]
+
+    def info(self, name):
+        dt, nd, nb = C.c_int(0), _sz(0), _sz(0)
+        shape = (_sz * 8)()
+        if self.L.fn["SNEPPX_qstore_info"](self.h, name.encode(), C.byref(dt), shape, C.byref(nd),
+                                           C.byref(nb)):
+            return None
+        return dt.value, tuple(shape[i] for i in range(nd.value)), nb.value
+
+    def host(self, name):
+        """Copy of a tensor's bytes as a numpy array of its dtype and shape."""
+        inf = self.info(name)
+        if inf is None:
+            raise KeyError(name)
+        dt, shape, nb = inf
+        n = _sz(0)
+        p = self.L.fn["SNEPPX_qstore_data"](self.h, name.encode(), C.byref(n))
+        raw = np.frombuffer(C.string_at(p, n.value), np.uint8) if n.value else np.zeros(0, np.uint8)
+        npdt = QST_NUMPY[QST_DTYPES[dt]] if 0 <= dt < len(QST_DTYPES) else np.uint8
+        return raw.view(npdt).reshape(shape) if dt >= 0 else raw
+
+    def metadata(self, key):
+        v = self.L.fn["SNEPPX_qstore_metadata"](self.h, key.encode())
+        return None if v is None else v.decode()
+
+    def read_device(self, name, t, stream=None):
+        self.L.check(self.L.fn["SNEPPX_qstore_read_device"](
+            self.h, name.encode(), _ptr(t), t.numel() * t.element_size(), self.L._stream(stream)),
+            "qstore_read_device")
+
+    def query_w4(self, prefix):
+        N, K, G = _sz(0), _sz(0), _sz(0)
+        group, hz, hg = C.c_int(0), C.c_int(0), C.c_int(0)
+        self.L.check(self.L.fn["SNEPPX_qstore_query_w4"](
+            self.h, prefix.encode(), C.byref(N), C.byref(K), C.byref(G), C.byref(group),
+            C.byref(hz), C.byref(hg)), "qstore_query_w4")
+        return N.value, K.value, G.value, group.value, bool(hz.value), bool(hg.value)
+
+    def load_w4(self, prefix, qweight, scales, qzeros=None, g_idx=None, stream=None):
+        self.L.check(self.L.fn["SNEPPX_qstore_load_w4"](
+            self.h, prefix.encode(), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx),
+            self.L._stream(stream)), "qstore_load_w4")
+
+    def query_w8(self, prefix):
+        N, K = _sz(0), _sz(0)
+        self.L.check(self.L.fn["SNEPPX_qstore_query_w8"](self.h, prefix.encode(), C.byref(N), C.byref(K)),
+                     "qstore_query_w8")
+        return N.value, K.value
+
+    def load_w8(self, prefix, q, scales, stream=None):
+        self.L.check(self.L.fn["SNEPPX_qstore_load_w8"](
+            self.h, prefix.encode(), _ptr(q), _ptr(scales), self.L._stream(stream)), "qstore_load_w8")
+
+
+class QStoreWriter:
+    """Accumulates tensors and metadata; close() writes the file."""
+
+    def __init__(self, lib, handle):
+        self.L, self.h = lib, C.c_void_p(handle)
+
+    def add_host(self, name, dtype, arr):
+        arr = np.array(arr, order="C", copy=True)   # keeps 0-d arrays 0-d
+        shape, nd = _shape_arg(arr.shape)
+        self.L.check(self.L.fn["SNEPPX_qstore_writer_add_host"](
+            self.h, name.encode(), QST_DTYPES.index(dtype), shape, nd, arr.ctypes.data_as(_vp)),
+            "qstore_writer_add_host")
+
+    def add_device(self, name, dtype, t, stream=None):
+        shape, nd = _shape_arg(tuple(t.shape))
+        self.L.check(self.L.fn["SNEPPX_qstore_writer_add_device"](
+            self.h, name.encode(), QST_DTYPES.index(dtype), shape, nd, _ptr(t), self.L._stream(stream)),
+            "qstore_writer_add_device")
+
+    def set_metadata(self, key, value):
+        self.L.check(self.L.fn["SNEPPX_qstore_writer_set_metadata"](self.h, key.encode(), value.encode()),
+                     "qstore_writer_set_metadata")
+
+    def save_w4(self, prefix, qweight, scales, qzeros, g_idx, N, K, group, G, stream=None):
+        self.L.check(self.L.fn["SNEPPX_qstore_save_w4"](
+            self.h, prefix.encode(), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), N, K,
+            group, G, self.L._stream(stream)), "qstore_save_w4")
+
+    def save_w8(self, prefix, q, scales, stream=None):
+        N, K = q.shape
+        self.L.check(self.L.fn["SNEPPX_qstore_save_w8"](
+            self.h, prefix.encode(), _ptr(q), _ptr(scales), N, K, self.L._stream(stream)), "qstore_save_w8")
+
+    def close(self):
+        h, self.h = self.h, None
+        if h:
+            self.L.check(self.L.fn["SNEPPX_qstore_writer_close"](h), "qstore_writer_close")
 
 
 _LIB = None
