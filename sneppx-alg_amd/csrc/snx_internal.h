@@ -57,6 +57,10 @@ int snx_k_fp8_decode(const uint8_t* c, float* y, size_t n, int fmt, void* stream
 /* rne: 0 = roundf (the reference), 1 = ties to even */
 int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows, size_t cols,
                           int rne, void* stream);
+/* layer_kernels.hip: out[c][r] = in[r][c] (in is rows x cols); fp32 -> bf16 RNE */
+int snx_k_transpose_f32(const float* in, float* out, size_t rows, size_t cols, void* stream);
+int snx_k_f32_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
+
 /* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
 int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,
                               void* stream);

@@ -107,6 +107,18 @@ EXPORTS = {
     "SNEPPX_qstore_load_w8": (C.c_int, [_vp, C.c_char_p, _vp, _vp, _vp]),
     "SNEPPX_quantize_int8_modelzoo": (C.c_int, [_f32p, _i8p, _sz, C.POINTER(C.c_float)]),
     "SNEPPX_dev_quantize_int8_modelzoo": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    # quantized layers for the reference's linear call sites (include/sneppx_qlayer.h)
+    "SNEPPX_qlayer_create_kn": (_vp, [_f32p, _sz, _sz, C.c_int, C.c_int, _vp]),
+    "SNEPPX_qlayer_create_kn_device": (_vp, [_vp, _sz, _sz, C.c_int, C.c_int, _vp]),
+    "SNEPPX_qlayer_load": (_vp, [_vp, C.c_char_p, _vp]),
+    "SNEPPX_qlayer_save": (C.c_int, [_vp, _vp, C.c_char_p, _vp]),
+    "SNEPPX_qlayer_destroy": (None, [_vp]),
+    "SNEPPX_qlayer_in_features": (_sz, [_vp]),
+    "SNEPPX_qlayer_out_features": (_sz, [_vp]),
+    "SNEPPX_qlayer_format": (C.c_int, [_vp]),
+    "SNEPPX_qlayer_forward_f32": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "SNEPPX_qlayer_forward_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
+    "SNEPPX_qlayer_matmul_host": (C.c_int, [_vp, _f32p, _f32p, _sz]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
@@ -378,6 +390,27 @@ class Library:
             raise SneppxError(f"qstore_writer_open failed: {self.last_error()}")
         return QStoreWriter(self, h)
 
+    # ---------------- quantized layers (reference [K, N] weights) ------------
+    def qlayer_create_kn(self, w_kn, fmt="w4", group=128, stream=None):
+        """w_kn: numpy fp32 [K, N] (host) or a torch fp32 [K, N] device tensor."""
+        code = {"w8": 0, "w4": 1}[fmt]
+        if isinstance(w_kn, np.ndarray):
+            w = np.ascontiguousarray(w_kn, np.float32)
+            K, N = w.shape
+            h = self.fn["SNEPPX_qlayer_create_kn"](w, K, N, code, group, self._stream(stream))
+        else:
+            K, N = w_kn.shape
+            h = self.fn["SNEPPX_qlayer_create_kn_device"](_ptr(w_kn), K, N, code, group, self._stream(stream))
+        if not h:
+            raise SneppxError(f"qlayer_create_kn failed: {self.last_error()}")
+        return QLayer(self, h)
+
+    def qlayer_load(self, store, prefix, stream=None):
+        h = self.fn["SNEPPX_qlayer_load"](store.h, prefix.encode(), self._stream(stream))
+        if not h:
+            raise SneppxError(f"qlayer_load failed: {self.last_error()}")
+        return QLayer(self, h)
+
     # ---------------- HIP events on an explicit stream ----------------------
     def event(self):
         e = C.c_void_p()
@@ -523,6 +556,48 @@ class QStoreWriter:
         h, self.h = self.h, None
         if h:
             self.L.check(self.L.fn["SNEPPX_qstore_writer_close"](h), "qstore_writer_close")
+
+
+class QLayer:
+    """SNEPPXQLayer: y = x . W for a reference-layout weight W [K, N]."""
+
+    def __init__(self, lib, handle):
+        self.L, self.h = lib, C.c_void_p(handle)
+        self.K = lib.fn["SNEPPX_qlayer_in_features"](self.h)
+        self.N = lib.fn["SNEPPX_qlayer_out_features"](self.h)
+        self.format = ["w8", "w4"][lib.fn["SNEPPX_qlayer_format"](self.h)]
+
+    def destroy(self):
+        if self.h:
+            self.L.fn["SNEPPX_qlayer_destroy"](self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
+    def forward_f32(self, x, y, stream=None):
+        M = x.shape[0]
+        self.L.check(self.L.fn["SNEPPX_qlayer_forward_f32"](self.h, _ptr(x), _ptr(y), M,
+                                                            self.L._stream(stream)), "qlayer_forward_f32")
+
+    def forward_bf16(self, x, y, stream=None):
+        M = x.shape[0]
+        self.L.check(self.L.fn["SNEPPX_qlayer_forward_bf16"](self.h, _ptr(x), _ptr(y), M,
+                                                             self.L._stream(stream)), "qlayer_forward_bf16")
+
+    def matmul_host(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        M = x.shape[0]
+        y = np.zeros((M, self.N), np.float32)
+        self.L.check(self.L.fn["SNEPPX_qlayer_matmul_host"](self.h, x, y, M), "qlayer_matmul_host")
+        return y
+
+    def save(self, writer, prefix, stream=None):
+        self.L.check(self.L.fn["SNEPPX_qlayer_save"](self.h, writer.h, prefix.encode(),
+                                                     self.L._stream(stream)), "qlayer_save")
 
 
 _LIB = None
