@@ -130,6 +130,20 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
 int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
                             SNEPPXStream stream);
 
+/* SNEPPX_qlinear_silu_mul fused with the per-token int8 quantizer the W8A8
+ * down projection needs (no reference counterpart; the rule is
+ * SNEPPX_quantize_int8_channel, quantize_int8.c:157-177, applied to the bf16
+ * rows SNEPPX_qlinear_silu_mul would write): q int8 [T][F], scales fp32 [T].
+ * One pass instead of SwiGLU + quantize.  F % 8 == 0, F <= 32768. */
+int SNEPPX_qlinear_silu_mul_quant_int8(const uint16_t* gate_up, int8_t* q, float* scales,
+                                       size_t T, size_t F, SNEPPXStream stream);
+
+/* Per-token int8 of bf16 activations (SNEPPX_quantize_int8_channel,
+ * quantize_int8.c:157-177, on the bf16 values): for C4 inputs that come out
+ * of a bf16 op.  in bf16 [rows][cols], q int8, scales fp32 [rows]. */
+int SNEPPX_dev_quantize_int8_channel_bf16(const uint16_t* in, int8_t* q, float* scales,
+                                          size_t rows, size_t cols, SNEPPXStream stream);
+
 /* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n]), acc = sum_k A*W in
  * int32 (exact).  A int8 [M][K] (per-token scales sA fp32 [M]), W int8 [N][K]
  * (per-channel sW fp32 [N]), out bf16 [M][N]. */

@@ -242,20 +242,27 @@ __global__ void k_fp8_decode(const uint8_t* __restrict__ c, float* __restrict__ 
 
 // ------------------------------------------------------- row / group codecs
 // quantize_int8.c:157-177: one block per row.
-template <bool RNE>
-__global__ void k_quant_int8_rows(const float* __restrict__ x, int8_t* __restrict__ q,
+__device__ __forceinline__ float load_f(const float* p) { return *p; }
+__device__ __forceinline__ float load_f(const uint16_t* p) {   // bf16 bits
+    return __builtin_bit_cast(float, (uint32_t)*p << 16);
+}
+
+template <bool RNE, typename T>
+__global__ void k_quant_int8_rows(const T* __restrict__ x, int8_t* __restrict__ q,
                                   float* __restrict__ scales, size_t rows, size_t cols) {
     __shared__ float sh[16];
     for (size_t r = blockIdx.x; r < rows; r += gridDim.x) {
-        const float* xr = x + r * cols;
+        const T* xr = x + r * cols;
         float m = 0.0f;
-        for (size_t c = threadIdx.x; c < cols; c += blockDim.x) m = nanless_max(m, fabsf(xr[c]));
+        for (size_t c = threadIdx.x; c < cols; c += blockDim.x) m = nanless_max(m, fabsf(load_f(xr + c)));
         m = block_reduce(m, nanless_max, sh);
         float s = m < FLT_MIN ? 1.0f : m / 127.0f;
         float inv = 1.0f / s;
         if (threadIdx.x == 0) scales[r] = s;
-        for (size_t c = threadIdx.x; c < cols; c += blockDim.x)
-            q[r * cols + c] = (int8_t)clampi(RNE ? rne_i32(xr[c] * inv) : round_i32(xr[c] * inv), -128, 127);
+        for (size_t c = threadIdx.x; c < cols; c += blockDim.x) {
+            const float v = load_f(xr + c) * inv;
+            q[r * cols + c] = (int8_t)clampi(RNE ? rne_i32(v) : round_i32(v), -128, 127);
+        }
         __syncthreads();
     }
 }
@@ -692,10 +699,17 @@ int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows,
                           int rne, void* st) {
     int grid = (int)(rows < 65536 ? rows : 65536);
     if (rne)
-        k_quant_int8_rows<true><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
+        k_quant_int8_rows<true, float><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
     else
-        k_quant_int8_rows<false><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
+        k_quant_int8_rows<false, float><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
     return snx_launch_check("k_quant_int8_rows");
+}
+
+int snx_k_quant_int8_rows_bf16(const uint16_t* x, int8_t* q, float* scales, size_t rows,
+                               size_t cols, void* st) {
+    int grid = (int)(rows < 65536 ? rows : 65536);
+    k_quant_int8_rows<false, uint16_t><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
+    return snx_launch_check("k_quant_int8_rows_bf16");
 }
 
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* st) {

@@ -21,6 +21,7 @@
 //     removes the bias and zero point exactly.
 #include <hip/hip_runtime.h>
 
+#include <cfloat>
 #include <cstdint>
 
 #include "codec.h"
@@ -339,6 +340,16 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
 // SiLU(gate) * up between the gate/up and down projections of a SwiGLU MLP:
 // gu [T][2F] bf16 (gate in columns [0, F), up in [F, 2F)), out [T][F] bf16,
 // out = bf16(g / (1 + exp(-g)) * u) in fp32.  One thread per 8 columns.
+// Both kernels below call this one out-of-line function, so the fused
+// quantizer sees exactly the bf16 values k_silu_mul writes.
+__device__ __attribute__((noinline)) uint32_t silu_mul_pair(uint32_t gv, uint32_t uv) {
+    const float g0 = __builtin_bit_cast(float, gv << 16), g1 = __builtin_bit_cast(float, gv & 0xFFFF0000u);
+    const float u0 = __builtin_bit_cast(float, uv << 16), u1 = __builtin_bit_cast(float, uv & 0xFFFF0000u);
+    const float r0 = g0 / (1.0f + expf(-g0)) * u0;
+    const float r1 = g1 / (1.0f + expf(-g1)) * u1;
+    return (uint32_t)bf16_out(r0) | (uint32_t)bf16_out(r1) << 16;
+}
+
 __global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ gu,
                                                   uint16_t* __restrict__ out, int F, size_t items) {
     const size_t it = (size_t)blockIdx.x * 256 + threadIdx.x;
@@ -350,14 +361,68 @@ __global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ g
     const u32x4 uv = *reinterpret_cast<const u32x4*>(gu + t * (size_t)(2 * F) + F + f);
     u32x4 o;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        const float g0 = __builtin_bit_cast(float, gv[e] << 16), g1 = __builtin_bit_cast(float, gv[e] & 0xFFFF0000u);
-        const float u0 = __builtin_bit_cast(float, uv[e] << 16), u1 = __builtin_bit_cast(float, uv[e] & 0xFFFF0000u);
-        const float r0 = g0 / (1.0f + expf(-g0)) * u0;
-        const float r1 = g1 / (1.0f + expf(-g1)) * u1;
-        o[e] = (uint32_t)bf16_out(r0) | (uint32_t)bf16_out(r1) << 16;
-    }
+    for (int e = 0; e < 4; e++) o[e] = silu_mul_pair(gv[e], uv[e]);
     *reinterpret_cast<u32x4*>(out + t * (size_t)F + f) = o;
+}
+
+// SwiGLU followed by the per-token int8 quantizer of the W8A8 down
+// projection, one workgroup per token: the bf16 SwiGLU row goes to LDS, a
+// block reduction gives max|h|, and the codes follow the reference's
+// per-row rule (quantize_int8.c:157-177: scale = max/127, or 1 below
+// FLT_MIN; q = clamp(roundf(h * (1/scale)), -128, 127)) applied to the bf16
+// values.  F % 8 == 0, F <= 32768 (64 KB of LDS).
+__global__ void __launch_bounds__(256) k_silu_mul_quant_int8(const uint16_t* __restrict__ gu,
+                                                             int8_t* __restrict__ q,
+                                                             float* __restrict__ scales, int F) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint32_t* hrow = reinterpret_cast<uint32_t*>(smem);       // F/2 words of bf16 pairs
+    __shared__ float red[4];
+    const size_t t = blockIdx.x;
+    const uint16_t* g = gu + t * (size_t)(2 * F);
+    const int f8n = F >> 3;
+    float m = 0.0f;
+    for (int c = threadIdx.x; c < f8n; c += 256) {
+        const u32x4 gv = *reinterpret_cast<const u32x4*>(g + c * 8);
+        const u32x4 uv = *reinterpret_cast<const u32x4*>(g + F + c * 8);
+        u32x4 h;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = silu_mul_pair(gv[e], uv[e]);
+            // the scan skips NaN like the reference's `a > max_abs`
+            const float a0 = fabsf(__builtin_bit_cast(float, h[e] << 16));
+            const float a1 = fabsf(__builtin_bit_cast(float, h[e] & 0xFFFF0000u));
+            m = a0 > m ? a0 : m;
+            m = a1 > m ? a1 : m;
+        }
+        *reinterpret_cast<u32x4*>(hrow + c * 4) = h;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float v = __shfl_xor(m, o);
+        m = v > m ? v : m;
+    }
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = red[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) m = red[w] > m ? red[w] : m;
+    const float s = m < FLT_MIN ? 1.0f : m / 127.0f;
+    const float inv = 1.0f / s;
+    if (threadIdx.x == 0) scales[t] = s;
+    int8_t* qr = q + t * (size_t)F;
+    for (int c = threadIdx.x; c < f8n; c += 256) {
+        const u32x4 h = *reinterpret_cast<const u32x4*>(hrow + c * 4);
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int32_t c0 = clampi(round_i32(__builtin_bit_cast(float, h[e] << 16) * inv), -128, 127);
+            const int32_t c1 = clampi(round_i32(__builtin_bit_cast(float, h[e] & 0xFFFF0000u) * inv), -128, 127);
+            const uint32_t pair = ((uint32_t)c0 & 0xFFu) | (((uint32_t)c1 & 0xFFu) << 8);
+            if (e < 2) lo |= pair << (16 * e);
+            else hi |= pair << (16 * (e - 2));
+        }
+        *reinterpret_cast<uint2*>(qr + c * 8) = make_uint2(lo, hi);
+    }
 }
 
 }  // namespace
@@ -368,6 +433,16 @@ int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* 
     const size_t items = T * (F / 8);
     k_silu_mul<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(gu, out, (int)F, items);
     return snx_launch_check("k_silu_mul");
+}
+
+int snx_k_silu_mul_quant_int8(const uint16_t* gu, int8_t* q, float* scales, size_t T, size_t F,
+                              void* st) {
+    if (F > 32768 || T > 0x7fffffff) {
+        snx_set_error("silu_mul_quant_int8: F=%zu (max 32768) or T=%zu too large", F, T);
+        return -1;
+    }
+    k_silu_mul_quant_int8<<<(unsigned)T, 256, F * 2, S(st)>>>(gu, q, scales, (int)F);
+    return snx_launch_check("k_silu_mul_quant_int8");
 }
 
 

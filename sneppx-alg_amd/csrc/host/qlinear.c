@@ -247,6 +247,25 @@ int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, si
     return snx_k_silu_mul(gate_up, out, T, F, stream);
 }
 
+int SNEPPX_qlinear_silu_mul_quant_int8(const uint16_t* gate_up, int8_t* q, float* scales,
+                                       size_t T, size_t F, SNEPPXStream stream) {
+    REQUIRE(gate_up && q && scales, "qlinear_silu_mul_quant_int8: NULL pointer");
+    REQUIRE(T && F, "qlinear_silu_mul_quant_int8: empty shape");
+    REQUIRE(F % 8 == 0 && F <= 32768, "qlinear_silu_mul_quant_int8: F=%zu must be a multiple of 8, <= 32768", F);
+    REQUIRE(aligned16(gate_up) && ((uintptr_t)q & 7u) == 0,
+            "qlinear_silu_mul_quant_int8: gate_up must be 16-byte and q 8-byte aligned");
+    snx_clear_error();
+    return snx_k_silu_mul_quant_int8(gate_up, q, scales, T, F, stream);
+}
+
+int SNEPPX_dev_quantize_int8_channel_bf16(const uint16_t* in, int8_t* q, float* scales,
+                                          size_t rows, size_t cols, SNEPPXStream stream) {
+    REQUIRE(in && q && scales, "dev_quantize_int8_channel_bf16: NULL pointer");
+    REQUIRE(rows && cols, "dev_quantize_int8_channel_bf16: empty matrix");
+    snx_clear_error();
+    return snx_k_quant_int8_rows_bf16(in, q, scales, rows, cols, stream);
+}
+
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,
                            uint16_t* out, size_t M, size_t N, size_t K, SNEPPXStream stream) {
     REQUIRE(A && sA && W && sW && out, "qlinear_w8a8_i8: NULL pointer");

@@ -64,6 +64,9 @@ int snx_k_f32_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
 /* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
 int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,
                               void* stream);
+/* the same rule (roundf) on bf16 rows */
+int snx_k_quant_int8_rows_bf16(const uint16_t* x, int8_t* q, float* scales, size_t rows,
+                               size_t cols, void* stream);
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* stream);
 int snx_k_awq_quantize(const float* w, int8_t* q, float* scales, size_t rows, size_t cols,
                        size_t group, void* stream);
@@ -123,6 +126,9 @@ int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      size_t M, size_t N, size_t K, int group, size_t Mp, void* stream);
 
 /* SwiGLU step: out [T][F] = bf16(silu(gu[:, :F]) * gu[:, F:]), F % 8 == 0 */
+/* SwiGLU then per-token int8 of the bf16 result (F % 8 == 0, F <= 32768) */
+int snx_k_silu_mul_quant_int8(const uint16_t* gu, int8_t* q, float* scales, size_t T, size_t F,
+                              void* stream);
 int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* stream);
 
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,

@@ -77,6 +77,8 @@ EXPORTS = {
     "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz,
                                                 C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_silu_mul_quant_int8": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_dev_quantize_int8_channel_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -346,6 +348,18 @@ class Library:
         T, F2 = gate_up.shape
         self.check(self.fn["SNEPPX_qlinear_silu_mul"](
             _ptr(gate_up), _ptr(out), T, F2 // 2, self._stream(stream)), "qlinear_silu_mul")
+
+    def qlinear_silu_mul_quant_int8(self, gate_up, q, scales, stream=None):
+        T, F2 = gate_up.shape
+        self.check(self.fn["SNEPPX_qlinear_silu_mul_quant_int8"](
+            _ptr(gate_up), _ptr(q), _ptr(scales), T, F2 // 2, self._stream(stream)),
+            "qlinear_silu_mul_quant_int8")
+
+    def dev_quantize_int8_channel_bf16(self, x, q, scales, stream=None):
+        rows, cols = x.shape
+        self.check(self.fn["SNEPPX_dev_quantize_int8_channel_bf16"](
+            _ptr(x), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)),
+            "dev_quantize_int8_channel_bf16")
 
     def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None):
         M, K = A.shape

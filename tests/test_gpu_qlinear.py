@@ -408,6 +408,46 @@ def test_silu_mul(lib, T, F):
     assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-6)
 
 
+@pytest.mark.parametrize("T,F", [(1, 8), (37, 14336), (300, 1000), (2, 32768)])
+def test_silu_mul_quant_int8_equals_quantizing_the_silu_output(lib, oracle, T, F):
+    print(f"[gpu] silu_mul_quant_int8 T={T} F={F}", flush=True)
+    rng = np.random.default_rng(T + F)
+    gu = bf16_bits(rng.normal(0, 2, (T, 2 * F)).astype(np.float32))
+    if T >= 37:
+        gu[3] = 0                                            # an all-zero row: scale 1, codes 0
+        gu[5, :F] = bf16_bits(np.full(F, 60.0, np.float32))  # saturating gate
+    g = to_dev(gu)
+    h = torch.empty((T, F), dtype=torch.bfloat16, device=DEV)
+    q = torch.empty((T, F), dtype=torch.int8, device=DEV)
+    s = torch.empty(T, device=DEV)
+    lib.qlinear_silu_mul(g, h)
+    lib.qlinear_silu_mul_quant_int8(g, q, s)
+    torch.cuda.synchronize()
+    rc, qo, so = oracle.quantize_int8_channel(bf16_to_f32(u16(h)).reshape(T, F))
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 4096), (2048, 4096), (3, 14336)])
+def test_dev_int8_channel_bf16_bit_exact(lib, oracle, rows, cols):
+    rng = np.random.default_rng(rows * cols)
+    xb = bf16_bits(rng.normal(0, 3, (rows, cols)).astype(np.float32))
+    q = torch.empty((rows, cols), dtype=torch.int8, device=DEV)
+    s = torch.empty(rows, device=DEV)
+    lib.dev_quantize_int8_channel_bf16(to_dev(xb), q, s)
+    torch.cuda.synchronize()
+    rc, qo, so = oracle.quantize_int8_channel(bf16_to_f32(xb).reshape(rows, cols))
+    np.testing.assert_array_equal(q.cpu().numpy(), qo)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
+
+
+def test_silu_mul_quant_int8_rejects_bad_shapes(lib):
+    g = torch.zeros((2, 2 * 12), dtype=torch.int16, device=DEV)
+    with pytest.raises(Exception, match="multiple of 8"):
+        lib.qlinear_silu_mul_quant_int8(g, torch.empty((2, 12), dtype=torch.int8, device=DEV),
+                                        torch.empty(2, device=DEV))
+
+
 # ---------------------------------------------------------- QAT fake-quant
 @pytest.mark.parametrize("n,scale,bits", [(1, 0.5, 8), (1000, 0.02, 4), (1 << 20, 0.003, 8), (77, 1.0, 16)])
 def test_dev_fake_quant_bit_exact(lib, oracle, n, scale, bits):
