@@ -1,0 +1,75 @@
+/*
+ * sneppx_mx.h - MX (micro-scaling) formats on gfx950.
+ *
+ * The reference implements MX encode/decode in Python/numpy
+ * (bindings/python/SneppX_ALG/interface_bindings/mx_formats.py: quantize_mx,
+ * dequantize_mx, formats at :53-72).  These entry points compute the same
+ * packed codes and int8 scale exponents on the device, bit for bit, for 2-D
+ * tensors blocked along the last axis (the reference's default
+ * block_axis=-1): a [rows][cols] float32 tensor is padded with zeros to a
+ * multiple of the block size per row, every block of `block_size` elements
+ * shares a power-of-two exponent (int8, one per block, [rows][nblocks]), and
+ * the codes of all padded elements form one little-endian bitstream in
+ * row-major order.  With block size 0 (NVFP4, or an explicit 0) one exponent
+ * covers the tensor and the codes of the rows*cols elements are packed
+ * without padding.
+ *
+ * The reference's element formats use every exponent field for finite values
+ * (E4M3 reaches 480, E5M2 114688), unlike the OCP formats of the gfx950
+ * matrix cores; its fp4/fp6 formats coincide with OCP's, so only MXFP4 /
+ * MXFP6 codes decode on the matrix cores to the reference's values.
+ *
+ * Returns 0 / -1 (text in SNEPPX_qlinear_last_error()).
+ */
+#ifndef SNEPPX_MX_H
+#define SNEPPX_MX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "sneppx_qlinear.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* MXFormat of mx_formats.py:38-45, in the order of MX_FORMATS (:53-72) */
+typedef enum {
+    SNEPPX_MXFP8_E4M3 = 0,
+    SNEPPX_MXFP8_E5M2 = 1,
+    SNEPPX_MXFP6_E3M2 = 2,
+    SNEPPX_MXFP6_E2M3 = 3,
+    SNEPPX_MXFP4_E2M1 = 4,
+    SNEPPX_NVFP4_E2M1 = 5
+} SNEPPXMXFormat;
+
+/* Bits per element and default block size (0 = one scale per tensor). */
+int SNEPPX_mx_bits(SNEPPXMXFormat fmt);
+int SNEPPX_mx_default_block(SNEPPXMXFormat fmt);
+
+/* Sizes of the outputs for a [rows][cols] tensor; block_size 0 picks the
+ * format's default (so NVFP4 is per tensor).  -1 / 0 on a bad format or a
+ * block size that is not a multiple of 8. */
+size_t SNEPPX_mx_packed_bytes(SNEPPXMXFormat fmt, size_t rows, size_t cols, int block_size);
+size_t SNEPPX_mx_scale_count(SNEPPXMXFormat fmt, size_t rows, size_t cols, int block_size);
+
+/* quantize_mx (mx_formats.py:144-201).  x float32 [rows][cols] (device),
+ * packed uint8 and scales int8 (device) of the sizes above.  block_size: 0 =
+ * the format's default, otherwise a positive multiple of 8, or -1 for one
+ * scale per tensor.  Per-tensor quantization returns -1 where the reference
+ * raises (an infinite peak, an exponent outside int8) and waits for the
+ * device (the exponent is checked on the host). */
+int SNEPPX_dev_quantize_mx(const float* x, uint8_t* packed, int8_t* scales, size_t rows,
+                           size_t cols, SNEPPXMXFormat fmt, int block_size, SNEPPXStream stream);
+
+/* dequantize_mx (mx_formats.py:204-222): y float32 [rows][cols] = the
+ * reference's float64 result rounded to float32 (exact unless it overflows
+ * or underflows float32). */
+int SNEPPX_dev_dequantize_mx(const uint8_t* packed, const int8_t* scales, float* y, size_t rows,
+                             size_t cols, SNEPPXMXFormat fmt, int block_size, SNEPPXStream stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SNEPPX_MX_H */

@@ -61,6 +61,17 @@ int snx_k_quant_int8_rows(const float* x, int8_t* q, float* scales, size_t rows,
 int snx_k_transpose_f32(const float* in, float* out, size_t rows, size_t cols, void* stream);
 int snx_k_f32_to_bf16(const float* x, uint16_t* y, size_t n, void* stream);
 
+/* mx_kernels.hip (f: element format 0 e4m3, 1 e5m2, 2 e3m2, 3 e2m3, 4 e2m1) */
+int snx_mx_scale_host(uint32_t peak_bits, int f, int tensor);
+int snx_k_mx_quant_blocks(const float* x, uint8_t* packed, int8_t* scales, size_t rows,
+                          size_t cols, int bs, int f, void* stream);
+int snx_k_mx_dequant_blocks(const uint8_t* packed, const int8_t* scales, float* y, size_t rows,
+                            size_t cols, int bs, int f, void* stream);
+int snx_mx_tensor_parts(size_t n);
+int snx_k_mx_tensor_stats(const float* x, size_t n, uint32_t* part, int nparts, void* stream);
+int snx_k_mx_quant_tensor(const float* x, uint8_t* packed, size_t n, int s, int f, void* stream);
+int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* stream);
+
 /* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
 int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,
                               void* stream);

@@ -121,6 +121,13 @@ EXPORTS = {
     "SNEPPX_qlayer_forward_f32": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
     "SNEPPX_qlayer_forward_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
     "SNEPPX_qlayer_matmul_host": (C.c_int, [_vp, _f32p, _f32p, _sz]),
+    # MX formats (include/sneppx_mx.h)
+    "SNEPPX_mx_bits": (C.c_int, [C.c_int]),
+    "SNEPPX_mx_default_block": (C.c_int, [C.c_int]),
+    "SNEPPX_mx_packed_bytes": (_sz, [C.c_int, _sz, _sz, C.c_int]),
+    "SNEPPX_mx_scale_count": (_sz, [C.c_int, _sz, _sz, C.c_int]),
+    "SNEPPX_dev_quantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
+    "SNEPPX_dev_dequantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
@@ -425,6 +432,42 @@ class Library:
             raise SneppxError(f"qlayer_load failed: {self.last_error()}")
         return QLayer(self, h)
 
+    # ---------------- MX formats (mx_formats.py semantics) ------------------
+    def _mx_block(self, fmt, block_size):
+        # the reference's `block_size or spec.block_size`, per tensor when <= 0
+        if block_size is None:
+            return 0
+        return block_size if block_size > 0 else -1
+
+    def dev_quantize_mx(self, x, fmt, block_size=None, stream=None):
+        """x: float32 device tensor [rows, cols] (or [n]); returns (packed uint8,
+        scales int8) device tensors laid out as quantize_mx returns them."""
+        code = MX_FORMATS.index(fmt)
+        x2 = x if x.dim() == 2 else x.reshape(1, -1)
+        rows, cols = x2.shape
+        bs = self._mx_block(fmt, block_size)
+        nbytes = self.fn["SNEPPX_mx_packed_bytes"](code, rows, cols, bs)
+        nsc = self.fn["SNEPPX_mx_scale_count"](code, rows, cols, bs)
+        if nbytes == 0 or nsc == 0:
+            raise SneppxError(f"dev_quantize_mx: bad block size {block_size}")
+        packed = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        scales = torch.empty(nsc, dtype=torch.int8, device=x.device)
+        self.check(self.fn["SNEPPX_dev_quantize_mx"](
+            _ptr(x2), _ptr(packed), _ptr(scales), rows, cols, code, bs, self._stream(stream)),
+            "dev_quantize_mx")
+        if nsc > 1 or self.fn["SNEPPX_mx_default_block"](code) > 0 and bs >= 0:
+            scales = scales.reshape(rows, -1)
+        return packed, scales
+
+    def dev_dequantize_mx(self, packed, scales, shape, fmt, block_size=None, stream=None):
+        code = MX_FORMATS.index(fmt)
+        rows, cols = (1, shape[0]) if len(shape) == 1 else shape
+        y = torch.empty((rows, cols), dtype=torch.float32, device=packed.device)
+        self.check(self.fn["SNEPPX_dev_dequantize_mx"](
+            _ptr(packed), _ptr(scales), _ptr(y), rows, cols, code, self._mx_block(fmt, block_size),
+            self._stream(stream)), "dev_dequantize_mx")
+        return y.reshape(shape)
+
     # ---------------- HIP events on an explicit stream ----------------------
     def event(self):
         e = C.c_void_p()
@@ -446,6 +489,9 @@ class Library:
         self.check(self.fn["snx_hip_device_info"](buf, 128, C.byref(cu), C.byref(clk)), "device_info")
         return buf.value.decode(), cu.value, clk.value
 
+
+# SNEPPXMXFormat order (include/sneppx_mx.h = MX_FORMATS of mx_formats.py)
+MX_FORMATS = ["mxfp8_e4m3", "mxfp8_e5m2", "mxfp6_e3m2", "mxfp6_e2m3", "mxfp4_e2m1", "nvfp4_e2m1"]
 
 # dtype codes of include/sneppx_qstore.h (= the reference's SNEPPXSafetensorsDType)
 QST_DTYPES = ["F32", "F16", "F64", "I64", "I32", "I16", "I8", "U8", "BOOL", "BF16", "F8_E5M2",
