@@ -28,6 +28,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 INT8_PEAK_TOPS = 5033.2        # dense int8 MFMA (256 CU x 8192 op/clk x 2.4 GHz)
 FP8_PEAK_TOPS = 5033.2         # dense fp8 MFMA
 BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
+FP4_PEAK_TFLOPS = 10066.3      # dense fp4 MFMA (MXFP4)
 METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
 
 
@@ -41,7 +42,7 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -213,6 +214,23 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
             "tops_kernel": ops / mean_launch / 1e9}
 
 
+def bench_mxfp4(lib, timer, torch, M, N, K, steps, warmup):
+    """MXFP4 x MXFP4 GEMM (f4 row): operands quantized on the GPU with the
+    reference's MX rule, the product on the scaled fp4 matrix cores."""
+    g = torch.Generator(device="cuda").manual_seed(19)
+    a = torch.randn((M, K), device="cuda", generator=g)
+    w = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    pa, sa = lib.dev_quantize_mx(a, "mxfp4_e2m1")
+    pw, sw = lib.dev_quantize_mx(w, "mxfp4_e2m1")
+    del a, w
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    st = timer.stream
+    total, _, _ = timer.run([lambda: lib.qlinear_mxfp4_gemm(pa, sa, pw, sw, out, M, N, K, stream=st)],
+                            steps, warmup)
+    flops = 2 * M * N * K
+    return {"ms_per_step": total / steps, "tflops": flops / (total / steps) / 1e9}
+
+
 def bench_vendor_w8a8(torch, M, N, K, steps, warmup):
     """The same C4 shape through the vendor GEMM library (hipBLASLt behind
     torch._int_mm / torch._scaled_mm), timed the same way: a reference point
@@ -376,6 +394,9 @@ def run_only(args, lib, timer, torch, N, K, group):
         st = timer.stream
         t, _, _ = timer.run([lambda: lib.qlinear_w4a16(x, qw, sc, qz, None, K2 // 128, y, 128, stream=st)], steps, 2)
         print(f"gemm-w4 T={T} N={N2} K={K2}: {t / steps * 1e3:.1f} us, {2 * T * N2 * K2 / (t / steps) / 1e9:.0f} TFLOP/s")
+    elif args.only == "mx":
+        r = bench_mxfp4(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup)
+        print(f"mxfp4 gemm: {r['ms_per_step'] * 1e3:.1f} us, {r['tflops']:.0f} TFLOP/s")
     elif args.only == "chain":
         r = bench_chain(lib, timer, torch, steps, 2)
         print(f"chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s {r['per_linear']}")
@@ -463,6 +484,11 @@ def main():
                           "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4)})
         torch.cuda.synchronize()
         extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, 50, 30))
+        r = bench_mxfp4(lib, timer, torch, 2048, 14336, 4096, 50, 30)
+        extra.append({"workload": "MXFP4 x MXFP4 GEMM M=2048 N=14336 K=4096 (reference MX encoding, bf16 out)",
+                      "value": round(r["tflops"], 1), "unit": "TFLOP/s",
+                      "frac_of_peak": round(r["tflops"] / FP4_PEAK_TFLOPS, 4),
+                      "ms_per_step": round(r["ms_per_step"], 4)})
 
     cpu = None
     if not args.no_cpu:

@@ -10,9 +10,9 @@
  * multiple of the block size per row, every block of `block_size` elements
  * shares a power-of-two exponent (int8, one per block, [rows][nblocks]), and
  * the codes of all padded elements form one little-endian bitstream in
- * row-major order.  With block size 0 (NVFP4, or an explicit 0) one exponent
- * covers the tensor and the codes of the rows*cols elements are packed
- * without padding.
+ * row-major order.  With one exponent per tensor (NVFP4's default, or
+ * block_size -1) the codes of the rows*cols elements are packed without
+ * padding.
  *
  * The reference's element formats use every exponent field for finite values
  * (E4M3 reaches 480, E5M2 114688), unlike the OCP formats of the gfx950
@@ -67,6 +67,17 @@ int SNEPPX_dev_quantize_mx(const float* x, uint8_t* packed, int8_t* scales, size
  * or underflows float32). */
 int SNEPPX_dev_dequantize_mx(const uint8_t* packed, const int8_t* scales, float* y, size_t rows,
                              size_t cols, SNEPPXMXFormat fmt, int block_size, SNEPPXStream stream);
+
+/* MXFP4 x MXFP4 linear on the gfx950 scaled matrix cores (no reference
+ * counterpart; the reference stops at encode/decode): out[m][n] =
+ * sum_k A[m][k] W[n][k] where A [M][K] and W [N][K] are MXFP4 tensors as
+ * SNEPPX_dev_quantize_mx writes them with the default block of 32 (packed
+ * [rows][K/2] bytes, exponents [rows][K/32]).  out is bf16 or fp32 [M][N]
+ * (out_dtype SNEPPX_BFLOAT16 / SNEPPX_FLOAT32), fp32 accumulation; the fp4
+ * products are exact on the matrix cores.  K % 64 == 0. */
+int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                              const int8_t* sW, void* out, SNEPPXDtype out_dtype, size_t M,
+                              size_t N, size_t K, SNEPPXStream stream);
 
 #ifdef __cplusplus
 }

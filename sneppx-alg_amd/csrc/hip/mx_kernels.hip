@@ -324,3 +324,116 @@ int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, in
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// MXFP4 GEMM: out[m][n] = sum_k A[m][k] W[n][k] with A, W in the reference's
+// MXFP4 encoding (blocks of 32 along K, int8 exponents), on
+// v_mfma_scale_f32_32x32x64_f8f6f4 (E2M1 operands, E8M0 block scales, fp32
+// accumulators).  The E2M1 codes are the OCP ones, so the matrix cores see
+// exactly the reference's values; an int8 exponent s becomes the E8M0 byte
+// s + 127 (s = -128 is clamped to 2^-127).  Operand lane l: row / column
+// l % 32, elements 32 (l / 32) .. +31 of the 64-element step = 16 bytes of
+// codes and one scale byte (the block's exponent).
+// Workgroup: 128 x 128 outputs, 4 waves of 64 x 64 (2 x 2 blocks of 32);
+// every wave loads its fragments straight from global memory, the next K
+// step's while the current one computes.
+namespace {
+
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ inline int e8m0(int8_t s) { return s < -127 ? 0 : (int)s + 127; }
+
+template <bool YF32>
+__global__ void __launch_bounds__(256) k_mxfp4_gemm(const uint8_t* __restrict__ A,
+                                                    const int8_t* __restrict__ sA,
+                                                    const uint8_t* __restrict__ W,
+                                                    const int8_t* __restrict__ sW,
+                                                    void* __restrict__ out, int M, int N, int K) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r32 = lane & 31, h = lane >> 5;
+    const int m0 = blockIdx.y * 128 + (wave >> 1) * 64, n0 = blockIdx.x * 128 + (wave & 1) * 64;
+    const int kb = K / 32;   // scale blocks per row
+    int ra[2], rb[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int r = m0 + 32 * i + r32, c = n0 + 32 * i + r32;
+        ra[i] = r < M ? r : M - 1;
+        rb[i] = c < N ? c : N - 1;
+    }
+    auto load = [&](int ks, u32x4 (&fa)[2], u32x4 (&fb)[2], int (&sa)[2], int (&sb)[2]) {
+        const int blk = 2 * ks + h;   // this lane's 32-element block
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            fa[i] = *reinterpret_cast<const u32x4*>(A + (size_t)ra[i] * (K / 2) + (size_t)blk * 16);
+            fb[i] = *reinterpret_cast<const u32x4*>(W + (size_t)rb[i] * (K / 2) + (size_t)blk * 16);
+            sa[i] = e8m0(sA[(size_t)ra[i] * kb + blk]);
+            sb[i] = e8m0(sW[(size_t)rb[i] * kb + blk]);
+        }
+    };
+    f32x16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = f32x16{};
+    const int nks = K / 64;
+    u32x4 fa[2], fb[2];
+    int sa[2], sb[2];
+    load(0, fa, fb, sa, sb);
+    for (int ks = 0; ks < nks; ks++) {
+        u32x4 na[2], nb[2];
+        int nsa[2], nsb[2];
+        load(ks + 1 < nks ? ks + 1 : ks, na, nb, nsa, nsb);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+                const i32x8 a = {(int)fa[i][0], (int)fa[i][1], (int)fa[i][2], (int)fa[i][3], 0, 0, 0, 0};
+                const i32x8 b = {(int)fb[j][0], (int)fb[j][1], (int)fb[j][2], (int)fb[j][3], 0, 0, 0, 0};
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, b, acc[i][j], 4, 4, 0,
+                                                                            sa[i], 0, sb[j]);
+            }
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            fa[i] = na[i];
+            fb[i] = nb[i];
+            sa[i] = nsa[i];
+            sb[i] = nsb[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + 32 * j + r32;
+            if (n >= N) continue;
+#pragma unroll
+            for (int v = 0; v < 16; v++) {   // 32x32 C layout: row 8 (v/4) + 4 (l/32) + v%4
+                const int m = m0 + 32 * i + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (m >= M) continue;
+                if (YF32)
+                    reinterpret_cast<float*>(out)[(size_t)m * N + n] = acc[i][j][v];
+                else
+                    reinterpret_cast<uint16_t*>(out)[(size_t)m * N + n] =
+                        __builtin_bit_cast(uint16_t, (__bf16)acc[i][j][v]);
+            }
+        }
+}
+
+}  // namespace
+
+extern "C" int snx_k_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                                const int8_t* sW, void* out, int y_f32, size_t M, size_t N,
+                                size_t K, void* st) {
+    if (M > 0x7fffffff || N > 0x7fffffff || K > 0x7fffffff || (M + 127) / 128 > 65535) {
+        snx_set_error("mxfp4 gemm: shape too large");
+        return -1;
+    }
+    dim3 grid((unsigned)((N + 127) / 128), (unsigned)((M + 127) / 128));
+    if (y_f32)
+        k_mxfp4_gemm<true><<<grid, 256, 0, S(st)>>>(A, sA, W, sW, out, (int)M, (int)N, (int)K);
+    else
+        k_mxfp4_gemm<false><<<grid, 256, 0, S(st)>>>(A, sA, W, sW, out, (int)M, (int)N, (int)K);
+    return snx_launch_check("k_mxfp4_gemm");
+}

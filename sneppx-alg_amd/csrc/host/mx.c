@@ -116,3 +116,17 @@ int SNEPPX_dev_dequantize_mx(const uint8_t* packed, const int8_t* scales, float*
     if (snx_hip_memcpy_d2h(&s8, scales, 1, stream) || snx_hip_stream_sync(stream)) return -1;
     return snx_k_mx_dequant_tensor(packed, y, rows * cols, (int)s8, f, stream);
 }
+
+int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                              const int8_t* sW, void* out, SNEPPXDtype out_dtype, size_t M,
+                              size_t N, size_t K, SNEPPXStream stream) {
+    REQUIRE(A && sA && W && sW && out, "qlinear_mxfp4_gemm: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_mxfp4_gemm: empty shape");
+    REQUIRE(K % 64 == 0, "qlinear_mxfp4_gemm: K=%zu must be a multiple of 64", K);
+    REQUIRE(out_dtype == SNEPPX_BFLOAT16 || out_dtype == SNEPPX_FLOAT32,
+            "qlinear_mxfp4_gemm: out_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32");
+    REQUIRE(((uintptr_t)A & 15u) == 0 && ((uintptr_t)W & 15u) == 0,
+            "qlinear_mxfp4_gemm: A and W must be 16-byte aligned");
+    snx_clear_error();
+    return snx_k_mxfp4_gemm(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
+}

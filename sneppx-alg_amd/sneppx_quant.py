@@ -128,6 +128,7 @@ EXPORTS = {
     "SNEPPX_mx_scale_count": (_sz, [C.c_int, _sz, _sz, C.c_int]),
     "SNEPPX_dev_quantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
     "SNEPPX_dev_dequantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
+    "SNEPPX_qlinear_mxfp4_gemm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz, _vp]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
@@ -467,6 +468,12 @@ class Library:
             _ptr(packed), _ptr(scales), _ptr(y), rows, cols, code, self._mx_block(fmt, block_size),
             self._stream(stream)), "dev_dequantize_mx")
         return y.reshape(shape)
+
+    def qlinear_mxfp4_gemm(self, A, sA, W, sW, out, M, N, K, stream=None):
+        ydt = SNEPPX_FLOAT32 if out.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_mxfp4_gemm"](
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), ydt, M, N, K, self._stream(stream)),
+            "qlinear_mxfp4_gemm")
 
     # ---------------- HIP events on an explicit stream ----------------------
     def event(self):

@@ -87,3 +87,30 @@ def test_nonfinite_blocks_and_per_tensor_errors(lib):
 def test_rejects_block_sizes_that_are_not_byte_aligned(lib):
     with pytest.raises(Exception, match="block size"):
         lib.dev_quantize_mx(torch.zeros((2, 30), device=DEV), "mxfp6_e2m3", 12)
+
+
+@pytest.mark.parametrize("M,N,K,out", [(128, 128, 64, "f32"), (300, 200, 512, "f32"), (1, 4096, 4096, "bf16"),
+                                       (2048, 1024, 4096, "f32")])
+def test_mxfp4_gemm_against_dequantized_product(lib, M, N, K, out):
+    print(f"[gpu] mxfp4 gemm M={M} N={N} K={K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = (rng.normal(0, 0.02, (N, K)) * 10.0 ** rng.integers(-2, 2, (N, 1))).astype(np.float32)
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(a).to(DEV), "mxfp4_e2m1")
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(w).to(DEV), "mxfp4_e2m1")
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_mxfp4_gemm(pa, sa, pw, sw, y, M, N, K)
+    torch.cuda.synchronize()
+    da = mx.dequantize(pa.cpu().numpy(), sa.cpu().numpy(), (M, K), "mxfp4_e2m1")
+    dw = mx.dequantize(pw.cpu().numpy(), sw.cpu().numpy(), (N, K), "mxfp4_e2m1")
+    ref = da @ dw.T
+    got = y.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= (1e-5 if out == "f32" else 1e-2), err
+
+
+def test_mxfp4_gemm_rejects_k_not_multiple_of_64(lib):
+    z = torch.zeros(64, dtype=torch.uint8, device=DEV)
+    s = torch.zeros(8, dtype=torch.int8, device=DEV)
+    with pytest.raises(Exception, match="multiple of 64"):
+        lib.qlinear_mxfp4_gemm(z, s, z, s, torch.empty((2, 2), device=DEV), 2, 2, 96)
