@@ -16,6 +16,7 @@ TOPS, W4A16 at M=4/16, GPTQ act-order, the W8 GEMV).
 from __future__ import annotations
 
 import argparse
+import ctypes as C
 import json
 import os
 import sys
@@ -29,6 +30,7 @@ INT8_PEAK_TOPS = 5033.2        # dense int8 MFMA (256 CU x 8192 op/clk x 2.4 GHz
 FP8_PEAK_TOPS = 5033.2         # dense fp8 MFMA
 BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
 FP4_PEAK_TFLOPS = 10066.3      # dense fp4 MFMA (MXFP4)
+SNEPPX_BFLOAT16 = 3            # SNEPPXDtype of include/sneppx_qlinear.h
 METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
 
 
@@ -91,6 +93,17 @@ class Timer:
         return total_ms, sum(per) / len(per), per[len(per) // 2]
 
 
+def bound(lib, name, *args):
+    """A zero-argument launcher for one C entry point with its arguments
+    converted once (device pointers as c_void_p), so the timed loop measures
+    the GPU rather than Python's argument handling; checked once here."""
+    import ctypes as C
+    f = lib.fn[name]
+    conv = tuple(C.c_void_p(a.data_ptr()) if hasattr(a, "data_ptr") else a for a in args)
+    lib.check(f(*conv), name)
+    return lambda: f(*conv)
+
+
 def make_w4(lib, N, K, group, copies, seed, torch):
     g = torch.Generator(device="cuda").manual_seed(seed)
     w = torch.randn((N, K), device="cuda", generator=g) * 0.02
@@ -109,7 +122,8 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = timer.stream
-    calls = [lambda c=c: lib.qlinear_w4a16(x, c[0], c[1], c[2], None, G, y, group, stream=st) for c in ws]
+    calls = [bound(lib, "SNEPPX_qlinear_w4a16", x, c[0], c[1], c[2], None, G, y, SNEPPX_BFLOAT16,
+                   M, N, K, group, C.c_void_p(st)) for c in ws]
     total, mean_launch, med_launch = timer.run(calls, steps, warmup)
     nbytes = w4_bytes(M, N, K, G)
     return {
@@ -140,7 +154,8 @@ def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = timer.stream
-    calls = [lambda c=c: lib.qlinear_w4a16_actorder(x, c[0], c[1], None, order, y, 128, stream=st) for c in ws]
+    calls = [bound(lib, "SNEPPX_qlinear_w4a16_actorder", x, c[0], c[1], None, order, y,
+                   SNEPPX_BFLOAT16, M, N, K, 128, C.c_void_p(st)) for c in ws]
     total, mean_launch, _ = timer.run(calls, steps, warmup)
     nbytes = w4_bytes(M, N, K, G, zeros=False) + K * 2      # + uint16 perm
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
@@ -164,7 +179,7 @@ def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
     x = torch.randn((1, K), device="cuda", generator=g)
     y = torch.empty((1, N), device="cuda")
     st = timer.stream
-    calls = [lambda c=c: lib.qlinear_w8_gemv(x, c[0], c[1], y, stream=st) for c in ws]
+    calls = [bound(lib, "SNEPPX_qlinear_w8_gemv", x, c[0], c[1], y, 1, N, K, C.c_void_p(st)) for c in ws]
     total, mean_launch, _ = timer.run(calls, steps, warmup)
     nbytes = N * K + N * 4 + K * 4 + N * 4
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
@@ -503,7 +518,7 @@ def main():
     # per-launch duration = back-to-back time / launches (>= kernel time; it
     # matches rocprofv3's kernel-trace average to within the launch gap)
     achieved = head["bytes"] / head["ms_per_step"] / 1e6
-    traffic = load_traffic("k_w4a16_gemv_small")
+    traffic = load_traffic("k_w4a16_gemv1")
     line = {
         "metric": METRIC,
         "value": round(head["gbs"], 1),
@@ -522,7 +537,7 @@ def main():
                    "bytes_per_step": head["bytes"], "device": arch, "cus": cus},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "k_w4a16_gemv_small", "algorithmic_bytes": head["bytes"],
+                     "kernel": "k_w4a16_gemv1", "algorithmic_bytes": head["bytes"],
                      "launch_us": round(head["ms_per_step"] * 1e3, 3),
                      "event_pair_us_median": round(head["launch_ms_median"] * 1e3, 3)},
         "cpu_baseline": cpu,

@@ -2,11 +2,12 @@
 //
 //  * W8 weight-only (C1): int8 [N][K] x fp32 activations; 16-byte loads per
 //    lane, bytes converted in registers, per-channel scale applied once.
-//  * W4A16 (C2/C3/C5 decode): packed uint4 [N][K/8] x bf16 activations on
-//    v_mfma_f32_16x16x32_bf16.  Nibbles become bf16 (128 + q) with one
-//    and-or per pair; a second MFMA against the broadcast constant
-//    -(128 + z) removes the bias and zero point exactly, so the fp16 group
-//    scale is applied once per 128-column group in fp32.
+//  * W4A16 (C2/C3/C5 decode): packed uint4 [N][K/8] x bf16 activations.
+//    Nibbles become bf16 (128 + q) with one and-or per pair; the bias and
+//    zero point come off exactly in fp32 and the fp16 group scale is applied
+//    once per group.  M = 1 runs on the diagonal of
+//    v_mfma_f32_4x4x4bf16_1k (k_w4a16_gemv1), larger M on
+//    v_mfma_f32_16x16x32_bf16.
 //  * A generic W4A16 kernel (any group size, any g_idx, any M) as fallback.
 #include <hip/hip_runtime.h>
 
@@ -466,6 +467,233 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     }
 }
 
+// Full-wave sum with DPP moves (no LDS traffic); the total lands in lane 63.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_mv(float a) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), CTRL,
+                                                                 ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
+    v += dpp_mv<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mv<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mv<0x141, 0xF>(v);   // row_half_mirror
+    v += dpp_mv<0x140, 0xF>(v);   // row_mirror: every lane of a 16-lane row holds the row sum
+    v += dpp_mv<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_mv<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// M = 1 decode GEMV, group 128, K = 2048 T.  A workgroup (8 waves) owns 16
+// output rows, each wave 2 of them; lane l of a wave covers the 32-column
+// chunks c = 64 t + l (16 bytes of a row, one 16-byte load), so a wave load
+// instruction reads 1 KB of one row and the lane's columns are the same for
+// both rows.  The product runs on v_mfma_f32_4x4x4bf16_1k with only its
+// diagonal used: block b = lanes 4b..4b+3, A = the lane's unpacked weights,
+// B = the lane's own activations, so D[b][j][j] (lane 4b+j, element j) is
+// the lane's partial dot product - a quarter of the outputs of an
+// instruction that does a sixteenth of the work of a 16x16x32 one.
+// Activations are staged once per workgroup in LDS in MFMA k-slot order with
+// their 32-column sums; scales and zero words of the 16 rows are staged raw
+// beside them.  Every activation, scale and zero load is issued before any
+// weight load of the workgroup (s_barrier between them), because a CU
+// returns its loads in issue order; the weight loads are nontemporal.
+// PERM: the columns of qw are stored in the order perm (uint16 [K]), so the
+// activations are gathered x[perm[k']] from LDS before staging.
+template <int T, bool ZEROS, bool YF32, bool PERM>
+__global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict__ x,
+                                                     const uint32_t* __restrict__ qw,
+                                                     const uint16_t* __restrict__ scales,
+                                                     const uint32_t* __restrict__ qz,
+                                                     const uint16_t* __restrict__ perm,
+                                                     void* __restrict__ y, int N) {
+    constexpr int K = 2048 * T, G = 16 * T, KW = K / 8, NCH = K / 32, NIT = K / 8;
+    constexpr int RW = 2, WROWS = 16, NTHR = 512;
+    constexpr int XPT = (NIT + NTHR - 1) / NTHR;
+    constexpr int SPR = 2 * T, ZPR = 2 * T;                  // 16 B scale pieces, zero words per row
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* xsum = reinterpret_cast<float*>(smem + NCH * 80);             // [NCH]
+    uint32_t* ssc = reinterpret_cast<uint32_t*>(xsum + NCH);             // [16 rows][G/2 words]
+    uint32_t* szr = ssc + WROWS * (G / 2);                               // [16 rows][2T words]
+    uint16_t* xraw = reinterpret_cast<uint16_t*>(szr + WROWS * ZPR);     // PERM: [K]
+    uint16_t* pl = xraw + K;                                             // PERM: [K]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wg0 = blockIdx.x * WROWS;
+    const int n0 = wg0 + wave * RW;
+
+    // 1. activations (and perm), then the raw scales / zero words of the 16 rows
+    u32x4 xr[XPT], pr[PERM ? XPT : 1];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        int it = tid + i * NTHR;
+        it = it < NIT ? it : NIT - 1;
+        xr[i] = load16(x + (size_t)it * 8);
+        if (PERM) pr[i] = load16(perm + (size_t)it * 8);
+    }
+    u32x4 sv = {0u, 0u, 0u, 0u};
+    uint32_t zv = 0u;
+    const bool sload = tid < WROWS * SPR;
+    const bool zload = ZEROS && tid >= WROWS * SPR && tid < WROWS * (SPR + ZPR);
+    if (sload) {
+        int row = wg0 + tid / SPR;
+        row = row < N ? row : N - 1;
+        sv = load16(scales + (size_t)row * G + (tid % SPR) * 8);
+    }
+    if (zload) {
+        const int j = tid - WROWS * SPR;
+        int row = wg0 + j / ZPR;
+        row = row < N ? row : N - 1;
+        zv = qz[(size_t)row * ZPR + j % ZPR];
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+
+    // 2. weights: RW rows x T chunks, all in flight
+    u32x4 wv[RW][T];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        int row = n0 + r < N ? n0 + r : N - 1;
+#pragma unroll
+        for (int t = 0; t < T; t++)
+            wv[r][t] = __builtin_nontemporal_load(
+                reinterpret_cast<const u32x4*>(qw + (size_t)row * KW + (64 * t + lane) * 4));
+    }
+    asm volatile("" ::: "memory");
+
+    // 3. staging
+    if (sload) *reinterpret_cast<u32x4*>(ssc + tid * 4) = sv;
+    if (zload) szr[tid - WROWS * SPR] = zv;
+    if (PERM) {
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int it = tid + i * NTHR;
+            if (it < NIT) {
+                *reinterpret_cast<u32x4*>(xraw + it * 8) = xr[i];
+                *reinterpret_cast<u32x4*>(pl + it * 8) = pr[i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            int it = tid + i * NTHR;
+            it = it < NIT ? it : NIT - 1;
+            const u32x4 pv = *reinterpret_cast<const u32x4*>(pl + it * 8);
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t lo = pv[e] & 0xFFFFu, hi = pv[e] >> 16;
+                lo = lo < (uint32_t)K ? lo : (uint32_t)K - 1u;   // the caller's perm stays in LDS bounds
+                hi = hi < (uint32_t)K ? hi : (uint32_t)K - 1u;
+                xr[i][e] = (uint32_t)xraw[lo] | (uint32_t)xraw[hi] << 16;
+            }
+        }
+    }
+    // k-slot order {0,4,1,5 | 2,6,3,7} per 8 columns; chunk c (4 items) at c * 80 bytes;
+    // chunk sums over the 4 items held by 4 consecutive lanes
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int it0 = tid + i * NTHR;
+        const bool live = it0 < NIT;
+        const int it = live ? it0 : NIT - 1;
+        u32x4 p;
+        p[0] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x05040100u);
+        p[1] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x07060302u);
+        p[2] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x05040100u);
+        p[3] = __builtin_amdgcn_perm(xr[i][3], xr[i][1], 0x07060302u);
+        if (live) *reinterpret_cast<u32x4*>(smem + (it >> 2) * 80 + (it & 3) * 16) = p;
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            sum += __builtin_bit_cast(float, xr[i][e] << 16) + __builtin_bit_cast(float, xr[i][e] & 0xFFFF0000u);
+        sum += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, sum), 0xB1, 0xF, 0xF, false));
+        sum += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, sum), 0x4E, 0xF, 0xF, false));
+        if (live && (it & 3) == 0) xsum[it >> 2] = sum;
+    }
+    __syncthreads();
+
+    // 4. this lane's activations, chunk sums, scales and zero-point correction
+    uint32_t xb[T][16];
+    float X[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        const int c = 64 * t + lane;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(smem + c * 80 + q * 16);
+            xb[t][4 * q] = v[0];
+            xb[t][4 * q + 1] = v[1];
+            xb[t][4 * q + 2] = v[2];
+            xb[t][4 * q + 3] = v[3];
+        }
+        X[t] = xsum[c];
+    }
+    float sc[RW][T], corr[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        corr[r] = 0.0f;
+        const int wr = wave * RW + r;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const int g = 16 * t + (lane >> 2);                 // group of chunk 64 t + lane
+            const uint32_t sw = ssc[wr * (G / 2) + (g >> 1)];
+            const float s = f16_to_f32((uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+            const uint32_t z = ZEROS ? (szr[wr * ZPR + (g >> 3)] >> (4 * (g & 7))) & 15u : 8u;
+            sc[r][t] = s;
+            corr[r] = fmaf(s * (float)(128u + z), X[t], corr[r]);
+        }
+    }
+
+    // 5. nibbles -> bf16 (128 + q), one and-or per pair; diagonal 4x4x4 MFMAs
+    uint32_t nib_mask, bf_bias;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    f32x4 y4[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        y4[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                const uint32_t w = wv[r][t][d];
+                const u32x2 a0 = {(w & nib_mask) | bf_bias, ((w >> 4) & nib_mask) | bf_bias};
+                const u32x2 a1 = {((w >> 8) & nib_mask) | bf_bias, ((w >> 12) & nib_mask) | bf_bias};
+                const u32x2 b0 = {xb[t][4 * d], xb[t][4 * d + 1]};
+                const u32x2 b1 = {xb[t][4 * d + 2], xb[t][4 * d + 3]};
+                acc = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a0),
+                                                             __builtin_bit_cast(s16x4, b0), acc, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a1),
+                                                             __builtin_bit_cast(s16x4, b1), acc, 0, 0, 0);
+            }
+            y4[r] += sc[r][t] * acc;
+        }
+    }
+
+    // 6. the lane's diagonal element, wave sum, one lane stores the rows
+    const int dg = lane & 3;
+    float out[RW];
+#pragma unroll
+    for (int r = 0; r < RW; r++) {
+        const float d = dg == 0 ? y4[r][0] : dg == 1 ? y4[r][1] : dg == 2 ? y4[r][2] : y4[r][3];
+        out[r] = dpp_sum_to_lane63(d - corr[r]);
+    }
+    if (lane == 63) {
+#pragma unroll
+        for (int r = 0; r < RW; r++) {
+            if (n0 + r >= N) break;
+            if (YF32)
+                reinterpret_cast<float*>(y)[n0 + r] = out[r];
+            else
+                reinterpret_cast<uint16_t*>(y)[n0 + r] = f32_to_bf16(out[r]);
+        }
+    }
+}
+
 // Split-K W4A16 for 5 <= M <= 16: workgroup (bx, s) owns output rows
 // [64 bx, +64) (16 per wave) and the K span [s kspan, +kspan).  It stages
 // only that span of the M activation rows in LDS (slot order, per-step
@@ -644,8 +872,48 @@ int launch_small_m(const W4Launch& a) {
     return launch_small_vs<XPT, MM, false, PERM>(a);
 }
 
+// k_w4a16_gemv1 applies: M = 1, group 128, K = 2048 T (T <= 4), 16-byte aligned scales.
+size_t gemv1_lds(size_t K, bool perm) {
+    const size_t nch = K / 32, g = K / 128;
+    return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
+}
+
+template <int T, bool PERM>
+int launch_gemv1_t(const W4Launch& a) {
+    dim3 grid((unsigned)((a.N + 15) / 16)), block(512);
+    const size_t lds = gemv1_lds((size_t)a.K, PERM);
+#define SNX_G1(Z, F)                                                                      \
+    k_w4a16_gemv1<T, Z, F, PERM><<<grid, block, lds, a.s>>>(a.x, a.qw, a.scales, a.qz, a.perm, \
+                                                            a.y, a.N)
+    if (a.qz) {
+        if (a.y_f32) SNX_G1(true, true);
+        else SNX_G1(true, false);
+    } else {
+        if (a.y_f32) SNX_G1(false, true);
+        else SNX_G1(false, false);
+    }
+#undef SNX_G1
+    return snx_launch_check("k_w4a16_gemv1");
+}
+
+bool gemv1_ok(const W4Launch& a) {
+    return a.M == 1 && a.group == 128 && a.K % 2048 == 0 && a.K <= 8192 &&
+           ((uintptr_t)a.scales & 15u) == 0 && ((uintptr_t)a.qz & 3u) == 0;
+}
+
+template <bool PERM>
+int launch_gemv1(const W4Launch& a) {
+    switch (a.K / 2048) {
+        case 1: return launch_gemv1_t<1, PERM>(a);
+        case 2: return launch_gemv1_t<2, PERM>(a);
+        case 3: return launch_gemv1_t<3, PERM>(a);
+        default: return launch_gemv1_t<4, PERM>(a);
+    }
+}
+
 template <int XPT, bool PERM>
 int launch_small(const W4Launch& a) {
+    if (gemv1_ok(a)) return launch_gemv1<PERM>(a);
     if (a.M == 1) return launch_small_m<XPT, 1, PERM>(a);
     if (a.M == 2) return launch_small_m<XPT, 2, PERM>(a);
     return launch_small_m<XPT, 4, PERM>(a);

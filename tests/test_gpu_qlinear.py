@@ -180,6 +180,25 @@ def test_w4a16_gemv_shapes(lib, oracle, M, N, K):
     assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
 
 
+@pytest.mark.parametrize("N,K,sym,out", [
+    (1, 2048, False, "f32"), (17, 4096, True, "bf16"), (1001, 6144, False, "f32"),
+    (300, 8192, True, "f32"), (16, 8192, False, "bf16"), (11008, 2048, False, "f32")])
+def test_w4a16_gemv_m1_group128(lib, oracle, N, K, sym, out):
+    # the M = 1, group-128 decode kernel at every K it takes (2048 T, T <= 4),
+    # row counts that leave part of the last workgroup empty, with and
+    # without zero points, fp32 and bf16 outputs
+    group = 128
+    print(f"[gpu] w4a16 gemv M=1 N={N} K={K} sym={sym} out={out}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, N + K, sym=sym)
+    x = bf16_bits(np.random.default_rng(K).normal(0, 1, (1, K)).astype(np.float32))
+    y = torch.empty((1, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None if sym else to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, None if sym else qz, None, N, K, group)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
 def test_w4a16_gemv_symmetric_and_tails(lib, oracle):
     # symmetric zero 8 (no qzeros), N not a multiple of 16, K of 1024
     N, K, group, M = 45, 1024, 256, 3
@@ -237,12 +256,14 @@ def test_actorder_prepare_rejects_uneven_groups(lib, oracle):
         lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), 2, qs, perm)
 
 
-@pytest.mark.parametrize("M,ydt", [(1, torch.float32), (1, torch.bfloat16), (3, torch.float32),
-                                   (4, torch.bfloat16), (8, torch.float32), (300, torch.float32)])
-def test_w4a16_actorder_prepared(lib, oracle, M, ydt):
+@pytest.mark.parametrize("M,ydt,K", [(1, torch.float32, 4096), (1, torch.bfloat16, 4096),
+                                     (1, torch.float32, 8192), (1, torch.float32, 2048),
+                                     (3, torch.float32, 4096), (4, torch.bfloat16, 4096),
+                                     (8, torch.float32, 4096), (300, torch.float32, 4096)])
+def test_w4a16_actorder_prepared(lib, oracle, M, ydt, K):
     """Prepared (group-contiguous) weights give the layer's result on the
     original column order: compared with the oracle on qweight + g_idx."""
-    N, K = 1040, 4096
+    N = 1040
     rng = np.random.default_rng(40 + M)
     g_idx = (rng.permutation(K) // 128).astype(np.int32)
     qw, sc, _, G = _w4_case(oracle, N, K, 128, 23, g_idx=g_idx)
