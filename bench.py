@@ -64,16 +64,24 @@ class Timer:
     def __init__(self, lib, stream):
         self.lib, self.stream = lib, stream
 
-    def run(self, calls, steps, warmup):
+    def run(self, calls, steps, warmup, loop=None):
+        """Back-to-back time of `steps` calls between two events; `loop(n)`,
+        when given, issues n calls from C (bench_loop.c) instead of Python."""
         import torch
-        for i in range(warmup):
-            calls[i % len(calls)]()
+        if loop:
+            loop(warmup)
+        else:
+            for i in range(warmup):
+                calls[i % len(calls)]()
         torch.cuda.synchronize()
         # whole-job time: back-to-back launches between two events
         a, b = self.lib.event(), self.lib.event()
         self.lib.record(a, self.stream)
-        for i in range(steps):
-            calls[i % len(calls)]()
+        if loop:
+            loop(steps)
+        else:
+            for i in range(steps):
+                calls[i % len(calls)]()
         self.lib.record(b, self.stream)
         total_ms = self.lib.elapsed_ms(a, b)
         torch.cuda.synchronize()
@@ -91,6 +99,44 @@ class Timer:
         self.lib.fn["snx_hip_event_destroy"](a)
         self.lib.fn["snx_hip_event_destroy"](b)
         return total_ms, sum(per) / len(per), per[len(per) // 2]
+
+
+_BENCHLIB = None
+
+
+def bench_loops():
+    """ctypes view of libsneppx_bench.so (C launch loops over the decode
+    entry points); None when it is not built."""
+    global _BENCHLIB
+    if _BENCHLIB is None:
+        path = os.path.join(REPO, "sneppx-alg_amd", "libsneppx_bench.so")
+        _BENCHLIB = C.CDLL(path) if os.path.exists(path) else False
+        if _BENCHLIB:
+            for name in ("snxb_loop_w4a16", "snxb_loop_w4a16_actorder", "snxb_loop_w8_gemv"):
+                getattr(_BENCHLIB, name).restype = C.c_int
+    return _BENCHLIB or None
+
+
+def ptr_array(tensors):
+    arr = (C.c_void_p * len(tensors))()
+    for i, t in enumerate(tensors):
+        arr[i] = t.data_ptr()
+    return arr
+
+
+def make_loop(name, *args):
+    """A loop(n) that issues n calls of a decode entry point from C, or None."""
+    bl = bench_loops()
+    if bl is None:
+        return None
+    f = getattr(bl, name)
+    conv = [C.c_void_p(a.data_ptr()) if hasattr(a, "data_ptr") else
+            (C.c_size_t(a) if isinstance(a, int) and not isinstance(a, bool) else a) for a in args]
+
+    def loop(n):
+        if f(C.c_int(n), *conv) != 0:
+            raise RuntimeError(f"{name} failed")
+    return loop
 
 
 def bound(lib, name, *args):
@@ -124,7 +170,10 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
     st = timer.stream
     calls = [bound(lib, "SNEPPX_qlinear_w4a16", x, c[0], c[1], c[2], None, G, y, SNEPPX_BFLOAT16,
                    M, N, K, group, C.c_void_p(st)) for c in ws]
-    total, mean_launch, med_launch = timer.run(calls, steps, warmup)
+    qwa, sca, qza = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws]), ptr_array([c[2] for c in ws])
+    loop = make_loop("snxb_loop_w4a16", C.c_int(len(ws)), x, qwa, sca, qza, y, C.c_int(SNEPPX_BFLOAT16),
+                     M, N, K, C.c_int(group), C.c_void_p(st))
+    total, mean_launch, med_launch = timer.run(calls, steps, warmup, loop)
     nbytes = w4_bytes(M, N, K, G)
     return {
         "bytes": nbytes, "ms_per_step": total / steps, "launch_ms_mean": mean_launch,
@@ -156,7 +205,10 @@ def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
     st = timer.stream
     calls = [bound(lib, "SNEPPX_qlinear_w4a16_actorder", x, c[0], c[1], None, order, y,
                    SNEPPX_BFLOAT16, M, N, K, 128, C.c_void_p(st)) for c in ws]
-    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    qwa, sca = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws])
+    loop = make_loop("snxb_loop_w4a16_actorder", C.c_int(len(ws)), x, qwa, sca, order, y,
+                     C.c_int(SNEPPX_BFLOAT16), M, N, K, C.c_int(128), C.c_void_p(st))
+    total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
     nbytes = w4_bytes(M, N, K, G, zeros=False) + K * 2      # + uint16 perm
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
             "gbs_kernel": nbytes / mean_launch / 1e6}
@@ -180,7 +232,9 @@ def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
     y = torch.empty((1, N), device="cuda")
     st = timer.stream
     calls = [bound(lib, "SNEPPX_qlinear_w8_gemv", x, c[0], c[1], y, 1, N, K, C.c_void_p(st)) for c in ws]
-    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    loop = make_loop("snxb_loop_w8_gemv", C.c_int(len(ws)), x, ptr_array([c[0] for c in ws]),
+                     ptr_array([c[1] for c in ws]), y, 1, N, K, C.c_void_p(st))
+    total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
     nbytes = N * K + N * 4 + K * 4 + N * 4
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
             "gbs_kernel": nbytes / mean_launch / 1e6, "codes_differing_half_even": mismatch}

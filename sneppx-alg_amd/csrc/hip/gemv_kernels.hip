@@ -77,68 +77,99 @@ __global__ void __launch_bounds__(256) k_w8_gemv(const float* __restrict__ x,
     }
 }
 
-// M = 1, K = 1024 SL: a workgroup of 4 waves stages x (fp32) once in LDS;
-// each wave owns R rows and issues all R x SL of its 16-byte weight loads
-// (lane l: bytes [16 l, +16) of every 1 KB slice) before the first FMA.
-// Bytes are read as unsigned (b ^ 0x80 = b + 128) with v_cvt_f32_ubyte*,
-// and 128 * sum(x) is taken off at the end:
-// sum x*b = sum x*(b + 128) - 128 * sum x.
-template <int R, int SL>
-__global__ void __launch_bounds__(256) k_w8_gemv1(const float* __restrict__ x,
-                                                  const int8_t* __restrict__ q,
-                                                  const float* __restrict__ s,
-                                                  float* __restrict__ y, int N, int K) {
-    extern __shared__ __attribute__((aligned(16))) float xl[];   // [K]
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_mv(float a) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), CTRL,
+                                                                 ROW_MASK, 0xF, false));
+}
+
+// Full-wave sum with DPP moves (no LDS traffic); the total lands in lane 63.
+__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
+    v += dpp_mv<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v += dpp_mv<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v += dpp_mv<0x141, 0xF>(v);   // row_half_mirror
+    v += dpp_mv<0x140, 0xF>(v);   // row_mirror: every lane of a 16-lane row holds the row sum
+    v += dpp_mv<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
+    v += dpp_mv<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+    return v;
+}
+
+// M = 1, K = 1024 SL: a workgroup of 16 waves (one output row each) stages
+// x (fp32) once in LDS and sums it; lane l of a wave loads bytes
+// [16 l, +16) of every 1 KB slice of its row (nontemporal 16-byte loads, all
+// SL in flight before the first FMA).  Bytes are read as unsigned
+// (b ^ 0x80 = b + 128) with v_cvt_f32_ubyte*, and 128 * sum(x) comes off
+// the wave total: sum x*b = sum x*(b + 128) - 128 * sum x.  The lane's 16
+// activations of a slice sit at (slice * 64 + lane) * 80 bytes, so the
+// 16-byte LDS reads of a wave are free of bank conflicts.  Summing x once
+// per workgroup instead of per lane removes a 16*SL-long dependent add chain
+// from every wave.
+template <int SL>
+__global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
+                                                   const int8_t* __restrict__ q,
+                                                   const float* __restrict__ s,
+                                                   float* __restrict__ y, int N) {
+    constexpr int K = 1024 * SL, NIT = K / 4, NTHR = 1024, XPT = (NIT + NTHR - 1) / NTHR;
+    extern __shared__ __attribute__((aligned(16))) float xl[];   // [SL * 64][20], then [16]
+    float* wsum = xl + SL * 64 * 20;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int n0 = (blockIdx.x * 4 + wave) * R;
+    const int n0 = blockIdx.x * 16 + wave;
+    const int n = n0 < N ? n0 : N - 1;
 
-    float4 xr[SL];   // x: K / 4 float4 = SL per thread
+    float4 xr[XPT];
 #pragma unroll
-    for (int i = 0; i < SL; i++) xr[i] = reinterpret_cast<const float4*>(x)[tid + 256 * i];
-    asm volatile("" ::: "memory");
-    u32x4 w[R][SL];
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        const int n = n0 + r < N ? n0 + r : N - 1;
-#pragma unroll
-        for (int sl = 0; sl < SL; sl++) w[r][sl] = load16(q + (size_t)n * K + sl * 1024 + lane * 16);
+    for (int i = 0; i < XPT; i++) {
+        int it = tid + i * NTHR;
+        it = it < NIT ? it : NIT - 1;
+        xr[i] = reinterpret_cast<const float4*>(x)[it];
     }
     asm volatile("" ::: "memory");
+    u32x4 w[SL];
 #pragma unroll
-    for (int i = 0; i < SL; i++) reinterpret_cast<float4*>(xl)[tid + 256 * i] = xr[i];
+    for (int sl = 0; sl < SL; sl++)
+        w[sl] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4*>(q + (size_t)n * K + sl * 1024 + lane * 16));
+    asm volatile("" ::: "memory");
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int it = tid + i * NTHR;
+        if (it < NIT) {
+            const int col = it * 4, sl = col >> 10, l = (col & 1023) >> 4, qq = (col & 15) >> 2;
+            reinterpret_cast<float4*>(xl)[(sl * 64 + l) * 5 + qq] = xr[i];
+            part += (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w);
+        }
+    }
+    part = dpp_sum_to_lane63(part);
+    if (lane == 63) wsum[wave] = part;
     __syncthreads();
 
-    float acc[R], xsum = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; r++) acc[r] = 0.0f;
+    float acc = 0.0f;
 #pragma unroll
     for (int sl = 0; sl < SL; sl++) {
         float xv[16];
 #pragma unroll
-        for (int t = 0; t < 16; t += 4) {
-            const float4 v = reinterpret_cast<const float4*>(xl + sl * 1024 + lane * 16)[t >> 2];
-            xv[t] = v.x; xv[t + 1] = v.y; xv[t + 2] = v.z; xv[t + 3] = v.w;
+        for (int t = 0; t < 4; t++) {
+            const float4 v = reinterpret_cast<const float4*>(xl)[(sl * 64 + lane) * 5 + t];
+            xv[4 * t] = v.x; xv[4 * t + 1] = v.y; xv[4 * t + 2] = v.z; xv[4 * t + 3] = v.w;
         }
 #pragma unroll
-        for (int t = 0; t < 16; t++) xsum += xv[t];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t u = w[r][sl][e] ^ 0x80808080u;
-                // (float)(byte j of u) compiles to one v_cvt_f32_ubyte<j>
-                acc[r] += xv[4 * e] * (float)(u & 0xFFu);
-                acc[r] += xv[4 * e + 1] * (float)((u >> 8) & 0xFFu);
-                acc[r] += xv[4 * e + 2] * (float)((u >> 16) & 0xFFu);
-                acc[r] += xv[4 * e + 3] * (float)(u >> 24);
-            }
+        for (int e = 0; e < 4; e++) {
+            const uint32_t u = w[sl][e] ^ 0x80808080u;
+            // (float)(byte j of u) compiles to one v_cvt_f32_ubyte<j>
+            acc += xv[4 * e] * (float)(u & 0xFFu);
+            acc += xv[4 * e + 1] * (float)((u >> 8) & 0xFFu);
+            acc += xv[4 * e + 2] * (float)((u >> 16) & 0xFFu);
+            acc += xv[4 * e + 3] * (float)(u >> 24);
         }
     }
+    acc = dpp_sum_to_lane63(acc);
+    if (lane == 63 && n0 < N) {
+        float xt = 0.0f;
 #pragma unroll
-    for (int r = 0; r < R; r++) {
-        const float v = wave_sum(acc[r] - 128.0f * xsum);
-        if (lane == 0 && n0 + r < N) y[n0 + r] = s[n0 + r] * v;
+        for (int i = 0; i < 16; i++) xt += wsum[i];
+        y[n0] = s[n0] * (acc - 128.0f * xt);
     }
 }
 
@@ -465,23 +496,6 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
         else
             reinterpret_cast<uint16_t*>(y)[(size_t)i * N + n0 + nl] = f32_to_bf16(v[i]);
     }
-}
-
-// Full-wave sum with DPP moves (no LDS traffic); the total lands in lane 63.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ float dpp_mv(float a) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, a), CTRL,
-                                                                 ROW_MASK, 0xF, false));
-}
-
-__device__ __forceinline__ float dpp_sum_to_lane63(float v) {
-    v += dpp_mv<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-    v += dpp_mv<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-    v += dpp_mv<0x141, 0xF>(v);   // row_half_mirror
-    v += dpp_mv<0x140, 0xF>(v);   // row_mirror: every lane of a 16-lane row holds the row sum
-    v += dpp_mv<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3
-    v += dpp_mv<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
-    return v;
 }
 
 // M = 1 decode GEMV, group 128, K = 2048 T.  A workgroup (8 waves) owns 16
@@ -1056,13 +1070,12 @@ int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs
 int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
                   size_t K, void* st) {
     if (M == 1 && (K == 1024 || K == 2048 || K == 4096 || K == 8192)) {
-        const size_t lds = K * sizeof(float);
-        const unsigned rows_per_wg = K <= 4096 ? 16 : 8;   // R = 4 (2 at K = 8192)
-        const unsigned grid = (unsigned)((N + rows_per_wg - 1) / rows_per_wg);
-        if (K == 1024) k_w8_gemv1<4, 1><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
-        else if (K == 2048) k_w8_gemv1<4, 2><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
-        else if (K == 4096) k_w8_gemv1<4, 4><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
-        else k_w8_gemv1<2, 8><<<grid, 256, lds, S(st)>>>(x, q, s, y, (int)N, (int)K);
+        const size_t lds = (K / 1024) * 64 * 20 * sizeof(float) + 16 * sizeof(float);
+        const unsigned grid = (unsigned)((N + 15) / 16);
+        if (K == 1024) k_w8_gemv1<1><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
+        else if (K == 2048) k_w8_gemv1<2><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
+        else if (K == 4096) k_w8_gemv1<4><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
+        else k_w8_gemv1<8><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
         return snx_launch_check("k_w8_gemv1");
     }
     if (K % 16 == 0) {
