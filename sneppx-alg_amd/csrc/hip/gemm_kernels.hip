@@ -472,6 +472,169 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
     }
 }
 
+// MXFP4 x MXFP4 (E2M1 codes, one E8M0 exponent per 32 elements) on
+// v_mfma_scale_f32_16x16x128_f8f6f4, staged like k_gemm_8w: 256 x 224 tiles,
+// 8 waves of 64 x 112, K stages of 128 bytes (256 elements) global -> LDS
+// with global_load_lds_dwordx4, double buffered.  Beside each stage sit the
+// stage's 8 scale bytes of every tile row (A rows then W rows, loaded with
+// 4-byte direct loads).  Lane (r16, q) takes 16-byte chunk 4h + q of its row
+// for k-step h - exactly one 32-element block, whose exponent is the lane's
+// MFMA scale operand (int8 s -> E8M0 s + 127).  The fp4 products are exact;
+// accumulation is fp32.
+constexpr int MXS_ROWS = TBM + TBN;               // scale rows per stage
+constexpr int MXS_STAGE = TLDS_STAGE + MXS_ROWS * 8;
+
+__device__ __forceinline__ int e8m0_of(int8_t s) { return s < -127 ? 0 : (int)s + 127; }
+
+template <bool YF32>
+__global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__ A,
+                                                     const int8_t* __restrict__ sA,
+                                                     const uint8_t* __restrict__ W,
+                                                     const int8_t* __restrict__ sW,
+                                                     void* __restrict__ out, int M, int N, int K,
+                                                     int tiles_m, int tiles_n) {
+    constexpr int FM = 4;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, q = lane >> 4;
+
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * TBM, n0 = tn * TBN;
+    const uint32_t KB = (uint32_t)K / 2, KS = (uint32_t)K / 32;   // bytes per row: codes, scales
+
+    const int lrow = lane >> 3, lslot = lane & 7;
+    uint32_t ga[4], gw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (8 * i + wave) * 8 + lrow;
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        ga[i] = (uint32_t)gr * KB + (uint32_t)((lslot ^ swz(row)) * 16);
+        const int wr = row < TBN ? row : TBN - 1;
+        const int gn = n0 + wr < N ? n0 + wr : N - 1;
+        gw[i] = (uint32_t)gn * KB + (uint32_t)((lslot ^ swz(wr)) * 16);
+    }
+    // scale dwords of a stage: 2 per row x 480 rows = 15 wave instructions;
+    // wave w issues instructions w and w + 8 (the latter for w < 7)
+    const int8_t* gs[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+        const int d = 64 * (wave + 8 * u) + lane, row = d >> 1, half = d & 1;
+        if (row < TBM) {
+            const int gr = m0 + row < M ? m0 + row : M - 1;
+            gs[u] = sA + (size_t)gr * KS + 4 * half;
+        } else {
+            const int r = row - TBM < TBN ? row - TBM : TBN - 1;
+            const int gn = n0 + r < N ? n0 + r : N - 1;
+            gs[u] = sW + (size_t)gn * KS + 4 * half;
+        }
+    }
+    auto dload = [&](int buf, int kt) {
+        int8_t* base = lds + buf * MXS_STAGE;
+        const uint32_t k0 = (uint32_t)kt * TBK;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
+        if (wave < 4)
+            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds(gs[0] + kt * 8, base + TLDS_STAGE + wave * 256, 4, 0, 0);
+        if (wave < 7)
+            __builtin_amdgcn_global_load_lds(gs[1] + kt * 8, base + TLDS_STAGE + (wave + 8) * 256, 4, 0, 0);
+    };
+
+    f32x4 acc[FM][TFN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < TFN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int sw = swz(r16);
+    const int8_t* arow = lds + (wm * 64 + r16) * TBK;
+    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
+    const int8_t* srow_a = lds + TLDS_STAGE + (wm * 64 + r16) * 8;
+    const int8_t* srow_w = lds + TLDS_STAGE + (TBM + wn * 112 + r16) * 8;
+    const int nk = K / (2 * TBK);
+
+    dload(0, 0);
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
+        __syncthreads();
+        dload(cur ^ 1, kt + 1 < nk ? kt + 1 : 0);   // last stage: stage 0 again, unused
+        const int8_t* ab = arow + cur * MXS_STAGE;
+        const int8_t* wb = wrow + cur * MXS_STAGE;
+        const int8_t* sa_ = srow_a + cur * MXS_STAGE;
+        const int8_t* sw_ = srow_w + cur * MXS_STAGE;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int c = 4 * h + q;
+            i32x8 fa[FM], fw[TFN];
+            int sca[FM], scw[TFN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const i32x4 v = lds16(ab + i * 16 * TBK + ((c ^ sw) << 4));
+                fa[i] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+                sca[i] = e8m0_of(sa_[i * 16 * 8 + c]);
+            }
+#pragma unroll
+            for (int j = 0; j < TFN; j++) {
+                const i32x4 v = lds16(wb + j * 16 * TBK + ((c ^ sw) << 4));
+                fw[j] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
+                scw[j] = e8m0_of(sw_[j * 16 * 8 + c]);
+            }
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                        fa[i], fw[j], acc[i][j], 4, 4, 0, sca[i], 0, scw[j]);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // the last (unused) loads drain before exit
+
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            const int n = n0 + wn * 112 + j * 16 + r16;
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+                if (m >= M) continue;
+                if (YF32)
+                    reinterpret_cast<float*>(out)[(size_t)m * N + n] = acc[i][j][e];
+                else
+                    reinterpret_cast<uint16_t*>(out)[(size_t)m * N + n] = bf16_out(acc[i][j][e]);
+            }
+        }
+    }
+}
+
+template <bool YF32>
+int launch_mxfp4_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                       void* out, int M, int N, int K, hipStream_t st) {
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+    const size_t lds = 2 * (size_t)MXS_STAGE;
+    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            snx_set_error("mxfp4 gemm: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+        attr_set = true;
+    }
+    k_mxfp4_tiled<YF32><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
+    return snx_launch_check("k_mxfp4_tiled");
+}
+
 // int8 on the 32x32 shape: same tile, LDS layout and direct loads as
 // k_gemm_8w, but the 8 waves split the tile along M only (wave w owns rows
 // [32 w, +32) and all 224 columns = 7 blocks of 32x32), so a stage issues
@@ -699,6 +862,16 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
     else
         k_i8_gemm<false><<<grid, 256, 0, S(st)>>>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K);
     return snx_launch_check("k_i8_gemm");
+}
+
+int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                           void* out, int y_f32, size_t M, size_t N, size_t K, void* st) {
+    if (K % 256 != 0 || (uint64_t)M * (K / 2) >= (1ull << 32) || (uint64_t)N * (K / 2) >= (1ull << 32)) {
+        snx_set_error("mxfp4 gemm: tiled kernel needs K %% 256 == 0 and operands below 4 GiB");
+        return -1;
+    }
+    if (y_f32) return launch_mxfp4_tiled<true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    return launch_mxfp4_tiled<false>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
 }
 
 int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const float* sW,

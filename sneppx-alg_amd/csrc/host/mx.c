@@ -128,5 +128,7 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
     REQUIRE(((uintptr_t)A & 15u) == 0 && ((uintptr_t)W & 15u) == 0,
             "qlinear_mxfp4_gemm: A and W must be 16-byte aligned");
     snx_clear_error();
+    if (K % 256 == 0 && M >= 128 && N >= 128 && ((uintptr_t)sA & 3u) == 0 && ((uintptr_t)sW & 3u) == 0)
+        return snx_k_mxfp4_gemm_tiled(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
     return snx_k_mxfp4_gemm(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
 }

@@ -72,6 +72,9 @@ int snx_k_mx_tensor_stats(const float* x, size_t n, uint32_t* part, int nparts, 
 int snx_k_mx_quant_tensor(const float* x, uint8_t* packed, size_t n, int s, int f, void* stream);
 int snx_k_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                      void* out, int y_f32, size_t M, size_t N, size_t K, void* stream);
+/* LDS-staged MXFP4 GEMM (256 x 224 tiles): K % 256 == 0, 4-byte aligned scales */
+int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                           void* out, int y_f32, size_t M, size_t N, size_t K, void* st);
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* stream);
 
 /* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
