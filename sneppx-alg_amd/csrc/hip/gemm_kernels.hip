@@ -4,6 +4,8 @@
 //    epilogue bf16((acc * sA[m]) * sW[n]) or the raw int32 tile.
 //  * fp8 e4m3 x e4m3 -> fp32 on v_mfma_f32_16x16x128_f8f6f4, epilogue
 //    bf16((acc * sA) * sW) with per-tensor scales read from device memory.
+//  * MXFP4 x MXFP4 (E2M1 codes, E8M0 block exponents) on the scaled
+//    v_mfma_scale_f32_16x16x128_f8f6f4, staged like the fp8 kernel.
 // Both operands are K-contiguous ("TN": A [M][K], W [N][K]).  Each MFMA lane
 // reads the K-bytes of its own row for A and of its own column for W at the
 // same k offsets, so A and B agree on every k-slot by construction.
