@@ -797,6 +797,228 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
     }
 }
 
+// Persistent int8 GEMM (the C4 int8 kernel).  Same tile, wave layout (8 waves
+// of 32 x 224), LDS ring, swizzle and MFMA as k_gemm_x32, but:
+//  * one workgroup per CU walks tiles b, b + nb, ... (nb = grid size, a
+//    multiple of 8, so every tile of a workgroup stays on its XCD);
+//  * operands go global -> LDS with buffer_load ... lds, counted by vmcnt
+//    only, so the fragment reads of k-step s + 1 stay in flight (lgkmcnt)
+//    across the MFMAs of k-step s instead of draining before each MFMA;
+//  * the last stage of a tile loads the next tile's stage 0 and, after the
+//    stage barrier, its first fragments; the epilogue then stages the bf16
+//    rows through the buffer the last stage freed (two passes of 16 rows per
+//    wave) and writes them with buffer stores (rows/columns outside the
+//    matrix get an out-of-range offset and are dropped), so the output write
+//    of tile i drains while tile i + 1 computes.
+// Barriers are raw s_barrier with explicit waits: a __syncthreads() fence
+// would also wait for the next stage's loads and the previous tile's stores.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every output buffer
+
+template <bool RAW>
+__global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
+                                                  const int8_t* __restrict__ W,
+                                                  const float* __restrict__ sA,
+                                                  const float* __restrict__ sW,
+                                                  int32_t* __restrict__ Craw,
+                                                  uint16_t* __restrict__ out, int M, int N, int K,
+                                                  int tiles_m, int tiles_n) {
+    constexpr int FN = TBN / 32;
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r32 = lane & 31, h = lane >> 5;
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int ntiles = tiles_m * tiles_n;
+    const int lrow = lane >> 3, lslot = lane & 7;
+    auto tile_of = [&](int t) { return (ntiles % 8 == 0) ? (t % 8) * (ntiles / 8) + t / 8 : t; };
+    // per-lane byte offsets of the direct loads (rows clamped into the matrix)
+    auto addr = [&](int t, uint32_t* ga, uint32_t* gw) {
+        const int tl = tile_of(t);
+        const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int row = (8 * i + wave) * 8 + lrow;
+            const int gr = m0 + row < M ? m0 + row : M - 1;
+            ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
+            const int wr = row < TBN ? row : TBN - 1;
+            const int gn = n0 + wr < N ? n0 + wr : N - 1;
+            gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
+        }
+    };
+    const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, N * K, 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, BUF_DROP, 0x00020000);
+    auto dload = [&](int buf, const uint32_t* ga, const uint32_t* gw, int k0) {
+        int8_t* base = lds + buf * TLDS_STAGE;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_ptr_t)(base + (8 * i + wave) * 1024), 16, ga[i], k0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + TLDS_A + (8 * i + wave) * 1024), 16, gw[i], k0, 0, 0);
+        if (wave < 4)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + TLDS_A + (24 + wave) * 1024), 16, gw[3], k0, 0, 0);
+    };
+    const int sw = swz(r32);
+    const int8_t* arow = lds + (wave * 32 + r32) * TBK;
+    const int8_t* wrow = lds + TLDS_A + r32 * TBK;
+    const int nk = K / TBK;
+    i32x16 acc[FN];
+    i32x4 fa[2], fw[2][FN];
+    // fragments of k-step s (chunk 2 s + h) of buffer buf into register slot
+    auto rd = [&](int slot, int buf, int s) {
+        const int off = ((2 * s + h) ^ sw) << 4;
+        fa[slot] = lds16(arow + buf * TLDS_STAGE + off);
+#pragma unroll
+        for (int j = 0; j < FN; j++) fw[slot][j] = lds16(wrow + buf * TLDS_STAGE + j * 32 * TBK + off);
+    };
+    auto mm = [&](int slot) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot], fw[slot][j], acc[j], 0, 0, 0);
+    };
+    // issue order inside a k-step: each MFMA followed by two fragment reads
+    // (and, in the first k-step, one direct load of the next stage)
+    auto pattern = [&](bool loads) {
+#pragma unroll
+        for (int q = 0; q < 7; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            if (q < 4) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            if (loads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        }
+    };
+    int t = b;
+    if (t >= ntiles) return;
+    uint32_t ga[4], gw[4];
+    addr(t, ga, gw);
+    dload(0, ga, gw, 0);
+    __builtin_amdgcn_s_waitcnt(0x0070);        // vmcnt(0) lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    int buf = 0;
+    rd(0, buf, 0);
+    for (;;) {
+        const int tl = tile_of(t);
+        const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
+        const int tnext = t + nb;
+        const bool has_next = tnext < ntiles;
+        float sa[16], swv[FN];
+        if (!RAW) {
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                sa[v] = sA[m < M ? m : M - 1];
+            }
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = n0 + j * 32 + r32;
+                swv[j] = sW[n < N ? n : N - 1];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[j] = i32x16{};
+        for (int kt = 0; kt < nk; kt++) {
+            const int cur = buf;
+            __builtin_amdgcn_sched_barrier(0);
+            if (kt + 1 < nk) {
+                dload(cur ^ 1, ga, gw, (kt + 1) * TBK);
+            } else {       // the next tile's stage 0 (this tile's again if there is none)
+                if (has_next) addr(tnext, ga, gw);
+                dload(cur ^ 1, ga, gw, 0);
+            }
+            rd(1, cur, 1);
+            mm(0);
+            pattern(true);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(0, cur, 2);
+            mm(1);
+            pattern(false);
+            __builtin_amdgcn_sched_barrier(0);
+            rd(1, cur, 3);
+            mm(0);
+            pattern(false);
+            __builtin_amdgcn_sched_barrier(0);
+            // next stage landed and this wave's reads of this stage are done
+            __builtin_amdgcn_s_waitcnt(0x0070);
+            __builtin_amdgcn_s_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+            rd(0, cur ^ 1, 0);
+            mm(1);
+            pattern(false);
+            __builtin_amdgcn_sched_barrier(0);
+            buf = cur ^ 1;
+        }
+        // buffer buf ^ 1 (this tile's last stage) is free; buffer buf holds the
+        // next tile's stage 0 and fa/fw[0] its first fragments
+        if (RAW) {   // int32 accumulators (bit-exactness checks): direct stores
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = n0 + j * 32 + r32;
+                if (n >= N) continue;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {    // 32x32 C layout: row 8 (v/4) + 4 (l/32) + v%4
+                    const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (m < M) Craw[(size_t)m * N + n] = acc[j][v];
+                }
+            }
+        } else {
+            uint16_t* ct = reinterpret_cast<uint16_t*>(lds + (buf ^ 1) * TLDS_STAGE) + wave * (16 * XCROW);
+#pragma unroll
+            for (int p = 0; p < 2; p++) {         // rows 16 p .. 16 p + 15 of the wave's 32
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int v = 8 * p; v < 8 * p + 8; v++)
+                        ct[(8 * (v >> 2) + 4 * h + (v & 3) - 16 * p) * XCROW + j * 32 + r32] =
+                            bf16_out((float)acc[j][v] * sa[v] * swv[j]);
+#pragma unroll
+                for (int q = 0; q < 7; q++) {     // 16 rows x 28 pieces of 16 B = 7 x 64
+                    const int qd = q * 64 + lane;
+                    const int row = qd / 28, c = qd - row * 28;
+                    const int m = m0 + wave * 32 + 16 * p + row, n = n0 + c * 8;
+                    const i32x4 val = *reinterpret_cast<const i32x4*>(ct + row * XCROW + c * 8);
+                    const uint32_t off = (m < M && n < N) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 2u : BUF_DROP;
+                    __builtin_amdgcn_raw_buffer_store_b128(val, ro, off, 0, 0);
+                }
+            }
+        }
+        // staging reads done (lgkmcnt(0)) before the next tile reloads this buffer
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+        if (!has_next) break;
+        t = tnext;
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);       // the spare stage-0 loads land before exit
+}
+
+template <bool RAW>
+int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
+               uint16_t* out, int M, int N, int K, hipStream_t st) {
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+    const int ntiles = tiles_m * tiles_n;
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    // one workgroup per CU (rounded down to a multiple of 8: tiles keep their XCD)
+    int grid = ncu >= 8 ? ncu - ncu % 8 : ncu;
+    if (grid > ntiles) grid = ntiles;
+    const size_t lds = 2 * (size_t)TLDS_STAGE;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_i8p<RAW>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+            snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+        attr_set = true;
+    }
+    k_gemm_i8p<RAW><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K, tiles_m, tiles_n);
+    return snx_launch_check("k_gemm_i8p");
+}
+
 template <bool FP8, bool RAW>
 int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
                  int32_t* Craw, uint16_t* out, int M, int N, int K, hipStream_t st) {
@@ -854,8 +1076,14 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
         return -1;
     }
     if (K % TBK == 0 && M >= 128 && N >= 128) {
+        // the persistent kernel addresses operands with 31-bit buffer offsets
+        // and writes bf16 output in 16-byte row pieces
+        const bool fits = (uint64_t)M * K < (1ull << 31) && (uint64_t)N * K < (1ull << 31);
         if (c_i32)
-            return launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+            return fits ? launch_i8p<true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st))
+                        : launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+        if (fits && N % 8 == 0 && (reinterpret_cast<uintptr_t>(out_bf16) & 15) == 0 && (uint64_t)M * N * 2 < BUF_DROP)
+            return launch_i8p<false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
         return launch_x32<false, false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
     }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));

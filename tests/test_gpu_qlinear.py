@@ -398,6 +398,32 @@ def test_w8a8_i8_full_shape_subtiles(lib, oracle):
     assert np.array_equal(Cn[-64:, -64:], ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(2148, 7208, 384), (300, 1000, 128), (130, 7205, 256)])
+def test_w8a8_i8_persistent_ragged(lib, oracle, M, N, K):
+    # 297 tiles for 256 workgroups (several tiles per workgroup, tile order
+    # without the XCD grouping), ragged edge tiles, odd and single-stage K
+    # loops, and N % 8 != 0 (bf16 output through the non-persistent kernel).
+    print(f"[gpu] w8a8 i8 persistent {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    sA = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    sW = rng.uniform(1e-4, 1e-3, N).astype(np.float32)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w8a8_i8(to_dev(A), to_dev(sA), to_dev(W), to_dev(sW), out)
+    Cm = torch.empty((M, N), dtype=torch.int32, device=DEV)
+    lib.qlinear_i8_gemm_i32(to_dev(A), to_dev(W), Cm)
+    torch.cuda.synchronize()
+    Cn, outn = Cm.cpu().numpy(), bf16_to_f32(u16(out))
+    blocks = [(0, 0), (M - 64, N - 64), (M - 64, 0), (0, N - 64)]
+    blocks += [(int(rng.integers(0, M - 64)), int(rng.integers(0, N - 64))) for _ in range(6)]
+    for m0, n0 in blocks:
+        ref = oracle.i8_gemm_i32(A[m0:m0 + 64], W[n0:n0 + 64])
+        assert np.array_equal(Cn[m0:m0 + 64, n0:n0 + 64], ref), (m0, n0)
+        deq = oracle.w8a8_epilogue(ref, sA[m0:m0 + 64], sW[n0:n0 + 64])
+        assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], deq) <= TOL_BF16, (m0, n0)
+
+
 @pytest.mark.parametrize("M,N,K", [(64, 64, 128), (130, 200, 4096)])
 def test_fp8_gemm(lib, oracle, M, N, K):
     print(f"[gpu] fp8 gemm {M}x{N}x{K}", flush=True)
