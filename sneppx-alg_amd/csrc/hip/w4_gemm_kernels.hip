@@ -11,7 +11,7 @@
 //     128 rows x 32 columns = 4 blocks of v_mfma_f32_32x32x16_bf16, which
 //     runs at twice the rate of the 16x16x32 form on gfx950), K step 128.
 //     Activation, packed-weight, scale, zero-point and step-sum slices move
-//     global->LDS with global_load_lds through a three-stage ring; each wave
+//     global->LDS with buffer_load ... lds through a three-stage ring; each wave
 //     streams the next-but-one stage in one load per MFMA sub-step.
 //     Activation rows are 256 B with 16-byte chunks XOR-swizzled by
 //     (row & 15); 64-byte weight rows rotate their chunks by bsw(row); both
@@ -38,6 +38,7 @@ typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 constexpr int GBM = 128, GBN = 256, GBK = 128;
 constexpr int GLDS_A = GBM * GBK * 2;           // 32 KB of bf16 activations
@@ -161,29 +162,38 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     const int sn = scol < N ? scol : N - 1;
     const bool zload = ZEROS && wave >= 4;
     const int zw = (G + 7) >> 3;
-    const uint8_t* xpb = reinterpret_cast<const uint8_t*>(xp);
-    const uint8_t* qwb = reinterpret_cast<const uint8_t*>(qw);
+    // buffer resources: buffer_load ... lds is counted by vmcnt alone, so
+    // LDS fragment reads stay in flight while the loads of later stages fly
+    // (global_load_lds also counts in lgkmcnt and forces lgkmcnt(0) waits)
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc((void*)xp, (short)0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc((void*)qw, (short)0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc((void*)(ZEROS ? (const void*)qz : (const void*)scales),
+                                                                        (short)0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsc = __builtin_amdgcn_make_buffer_rsrc((void*)scales, (short)0, -1, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rxs = __builtin_amdgcn_make_buffer_rsrc((void*)xs, (short)0, -1, 0x00020000);
+    const uint32_t zoff = (uint32_t)sn * (uint32_t)zw * 4u, soff = (uint32_t)sn * (uint32_t)G * 2u;
+    const uint32_t xsoff = (uint32_t)(m0 + (wave & 1) * 64 + lane) * 4u;
     // load p (0..7) of the eight each wave issues for stage kt into ring slot buf
     auto dpart = [&](int buf, int kt, int p) {
         uint8_t* base = lds + buf * GRING;
         if (p < 4) {
-            __builtin_amdgcn_global_load_lds(xpb + (ga[p] + (uint32_t)kt * (GBK * 2)),
-                                             base + (8 * p + wave) * 1024, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr_t)(base + (8 * p + wave) * 1024), 16, ga[p],
+                                                     kt * (GBK * 2), 0, 0);
         } else if (p < 6) {
-            __builtin_amdgcn_global_load_lds(qwb + (gw[p - 4] + (uint32_t)kt * (GBK / 2)),
-                                             base + GOFF_B + (8 * (p - 4) + wave) * 1024, 16, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_ptr_t)(base + GOFF_B + (8 * (p - 4) + wave) * 1024), 16,
+                                                     gw[p - 4], kt * (GBK / 2), 0, 0);
         } else if (p == 6) {
             const int g = (kt * GBK) >> gshift;
             if (zload)
-                __builtin_amdgcn_global_load_lds(qz + (size_t)sn * zw + (g >> 3),
-                                                 base + GOFF_Z + 256 * (wave & 3), 4, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr_t)(base + GOFF_Z + 256 * (wave & 3)), 4,
+                                                         zoff + (uint32_t)(g >> 3) * 4u, 0, 0, 0);
             else
-                __builtin_amdgcn_global_load_lds(scales + (size_t)sn * G + (g & ~1),
-                                                 base + GOFF_S + 256 * (wave & 3), 4, 0, 0);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsc, (lds_ptr_t)(base + GOFF_S + 256 * (wave & 3)), 4,
+                                                         soff + (uint32_t)(g & ~1) * 2u, 0, 0, 0);
         } else {
             // step sums of the tile's 128 rows (each half loaded by four waves)
-            __builtin_amdgcn_global_load_lds(xs + (size_t)kt * Mp + m0 + (wave & 1) * 64 + lane,
-                                             base + GOFF_X + (wave & 1) * 256, 4, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rxs, (lds_ptr_t)(base + GOFF_X + (wave & 1) * 256), 4, xsoff,
+                                                     kt * Mp * 4, 0, 0);
         }
     };
     auto dload = [&](int buf, int kt) {
@@ -238,8 +248,11 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     dload(1, nk > 1 ? 1 : 0);
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt % GSTAGES;
-        __builtin_amdgcn_s_waitcnt(0x0078);   // vmcnt(8): stage kt landed, kt + 1 may fly
-        __syncthreads();                      // and every wave is done with stage kt - 1
+        // vmcnt(8): stage kt landed, kt + 1 may fly; lgkmcnt(0): this wave is
+        // done with stage kt - 1.  A raw barrier: a __syncthreads() fence would
+        // wait for stage kt + 1 as well.
+        __builtin_amdgcn_s_waitcnt(0x0078);
+        __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);    // nothing below moves above the wait
         const int kn = kt + 2 < nk ? kt + 2 : nk - 1;   // past the end: reload, unused
         const int nbuf = (kt + 2) % GSTAGES;
