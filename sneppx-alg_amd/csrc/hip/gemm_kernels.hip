@@ -27,6 +27,20 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Direct global -> LDS loads go through buffer_load ... lds: those count in
+// vmcnt only, while global_load_lds also counts in lgkmcnt and so makes the
+// compiler drain every LDS fragment read (lgkmcnt(0)) before each MFMA.
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t brsrc(const void* p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ void bload_lds(__amdgpu_buffer_rsrc_t r, void* dst, int bytes, uint32_t voff, uint32_t soff) {
+    if (bytes == 16)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff, soff, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 4, voff, soff, 0, 0);
+}
+
 // 16 bytes of row `r` at column k (zero beyond K; K % 16 == 0 is required).
 __device__ __forceinline__ i32x4 frag16(const int8_t* base, int rows, int r, int K, int k) {
     if (r >= rows || k >= K) return i32x4{0, 0, 0, 0};
@@ -125,214 +139,27 @@ __global__ void __launch_bounds__(256) k_fp8_gemm(const uint8_t* __restrict__ A,
         }
 }
 
-// ------------------------------------------------------------ tiled GEMM
-// Workgroup tile 256 (M) x 224 (N); 4 waves in 2 x 2, each 128 x 112 =
-// 8 x 7 MFMA blocks of 16 x 16.  K advances in 128-byte stages, double
-// buffered in LDS (2 x 60 KB).  Operands go global -> LDS directly
-// (global_load_lds_dwordx4: no staging registers, no ds_write): each wave
+// ------------------------------------------------------------ tiled GEMMs
+// Workgroup tile 256 (M) x 224 (N), 8 waves.  K advances in 128-byte stages,
+// double buffered in LDS (2 x 60 KB).  Operands go global -> LDS directly
+// (buffer_load_dwordx4 ... lds: no staging registers, no ds_write): each wave
 // instruction fills 8 rows x 128 B.  16-byte chunk c of tile row R sits at
 // slot c ^ swz(R), swz(R) = (R & 7) ^ ((R >> 3) & 1): it depends on R mod 16
 // only (fragment rows share it), and the 16 rows of a fragment read hit
-// distinct bank groups whether LDS serves 8 or 16 lanes a cycle.
-// Per stage: loads for stage t+1 issued first; k-half 0 MFMAs (next half's
-// fragments in flight); wait for the loads + barrier; k-half 1 MFMAs while
-// stage t+1's first fragments are read.  int8: v_mfma_i32_16x16x64_i8 per
-// k-half; fp8: the stage's one v_mfma_f32_16x16x128_f8f6f4 k-step split by
-// fragment rows 0-3 / 4-7.  Tiles are dealt so each XCD (workgroups go to
-// the 8 XCDs round-robin) owns a compact 8 x (tiles_n / 8) block.
+// distinct bank groups whether LDS serves 8 or 16 lanes a cycle.  Tiles are
+// dealt so each XCD (workgroups go to the 8 XCDs round-robin) owns a compact
+// 8 x (tiles_n / 8) block.
 constexpr int TBM = 256, TBN = 224, TBK = 128;
-constexpr int TFM = 8, TFN = 7;                          // fragments per wave
+constexpr int TFN = 7;                                   // 16-column fragments per wave (fp8)
 constexpr int TLDS_A = TBM * TBK, TLDS_B = TBN * TBK, TLDS_STAGE = TLDS_A + TLDS_B;
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
 __device__ __forceinline__ i32x4 lds16(const int8_t* p) { return *reinterpret_cast<const i32x4*>(p); }
 
-template <bool FP8, bool RAW>
-__global__ void __launch_bounds__(256) k_gemm_tiled(const int8_t* __restrict__ A,
-                                                    const int8_t* __restrict__ W,
-                                                    const float* __restrict__ sA,
-                                                    const float* __restrict__ sW,
-                                                    int32_t* __restrict__ Craw,
-                                                    uint16_t* __restrict__ out, int M, int N, int K,
-                                                    int tiles_m, int tiles_n) {
-    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
-    const int r16 = lane & 15, q = lane >> 4;
-
-    const int b = blockIdx.x, nb = gridDim.x;
-    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
-    const int tm = tile % tiles_m, tn = tile / tiles_m;
-    const int m0 = tm * TBM, n0 = tn * TBN;
-
-    // direct-load sources: wave w, instruction i fills tile rows
-    // 8*(4 i + w) .. +8; lane s takes row +s/8, slot s%8 <- chunk slot^swz(row)
-    const int lrow = lane >> 3, lslot = lane & 7;
-    uint32_t ga[8], gw[7];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const int row = (4 * i + wave) * 8 + lrow;
-        const int gr = m0 + row < M ? m0 + row : M - 1;
-        ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
-    }
-#pragma unroll
-    for (int i = 0; i < 7; i++) {
-        const int row = (4 * i + wave) * 8 + lrow;
-        const int gr = n0 + row < N ? n0 + row : N - 1;
-        gw[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
-    }
-    auto dload = [&](int buf, int k0) {
-        int8_t* base = lds + buf * TLDS_STAGE;
-#pragma unroll
-        for (int i = 0; i < 8; i++)
-            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (4 * i + wave) * 1024, 16, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 7; i++)
-            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (4 * i + wave) * 1024, 16, 0, 0);
-    };
-
-    typedef typename std::conditional<FP8, f32x4, i32x4>::type acc_t;
-    acc_t acc[TFM][TFN];
-#pragma unroll
-    for (int i = 0; i < TFM; i++)
-#pragma unroll
-        for (int j = 0; j < TFN; j++) acc[i][j] = acc_t{0, 0, 0, 0};
-
-    // fragment rows: R = wm*128 + i*16 + r16 (A), wn*112 + j*16 + r16 (W);
-    // swz(R) depends on r16 only, so the byte offset of chunk c is fixed per lane
-    const int sw = swz(r16);
-    const int8_t* arow = lds + (wm * 128 + r16) * TBK;
-    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
-    const int nk = K / TBK;
-
-    dload(0, 0);
-    __builtin_amdgcn_s_waitcnt(0x0070);      // vmcnt(0) lgkmcnt(0): stage 0 landed in LDS
-    __syncthreads();
-
-    if (!FP8) {
-        i32x4 fa[2][TFM], fw[2][TFN];
-        // fragments of stage 0, k-half 0: chunk q
-#pragma unroll
-        for (int i = 0; i < TFM; i++) fa[0][i] = lds16(arow + i * 16 * TBK + ((q ^ sw) << 4));
-#pragma unroll
-        for (int j = 0; j < TFN; j++) fw[0][j] = lds16(wrow + j * 16 * TBK + ((q ^ sw) << 4));
-        for (int kt = 0; kt < nk; kt++) {
-            const int cur = kt & 1;
-            const int8_t* ab = arow + cur * TLDS_STAGE;
-            const int8_t* wb = wrow + cur * TLDS_STAGE;
-            // loads for stage t+1 (the last stage re-reads stage 0: in
-            // bounds, never used) keep the loop body branch-free
-            dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
-            // k-half 1 fragments (chunk 4 + q) while k-half 0 computes
-#pragma unroll
-            for (int i = 0; i < TFM; i++) fa[1][i] = lds16(ab + i * 16 * TBK + (((4 + q) ^ sw) << 4));
-#pragma unroll
-            for (int j = 0; j < TFN; j++) fw[1][j] = lds16(wb + j * 16 * TBK + (((4 + q) ^ sw) << 4));
-#pragma unroll
-            for (int i = 0; i < TFM; i++)
-#pragma unroll
-                for (int j = 0; j < TFN; j++)
-                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[0][i], fw[0][j], (i32x4)acc[i][j], 0, 0, 0);
-            // stage t+1 landed (vmcnt) and this wave's reads of stage t are
-            // done (lgkmcnt) before any wave may overwrite stage t's buffer
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(0x0070);
-            __syncthreads();
-            __builtin_amdgcn_sched_barrier(0);
-            {
-                const int8_t* an = arow + (cur ^ 1) * TLDS_STAGE;
-                const int8_t* wnx = wrow + (cur ^ 1) * TLDS_STAGE;
-#pragma unroll
-                for (int i = 0; i < TFM; i++) fa[0][i] = lds16(an + i * 16 * TBK + ((q ^ sw) << 4));
-#pragma unroll
-                for (int j = 0; j < TFN; j++) fw[0][j] = lds16(wnx + j * 16 * TBK + ((q ^ sw) << 4));
-            }
-#pragma unroll
-            for (int i = 0; i < TFM; i++)
-#pragma unroll
-                for (int j = 0; j < TFN; j++)
-                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[1][i], fw[1][j], (i32x4)acc[i][j], 0, 0, 0);
-        }
-    } else {
-        // fp8: per lane 32 bytes = chunks 2q, 2q+1
-        auto rd32 = [&](const int8_t* rowp) {
-            const i32x4 lo = lds16(rowp + (((2 * q) ^ sw) << 4));
-            const i32x4 hi = lds16(rowp + (((2 * q + 1) ^ sw) << 4));
-            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        };
-        i32x8 fw[2][TFN], fa[TFM];
-#pragma unroll
-        for (int j = 0; j < TFN; j++) fw[0][j] = rd32(wrow + j * 16 * TBK);
-#pragma unroll
-        for (int i = 0; i < 4; i++) fa[i] = rd32(arow + i * 16 * TBK);
-        for (int kt = 0; kt < nk; kt++) {
-            const int cur = kt & 1;
-            const int8_t* ab = arow + cur * TLDS_STAGE;
-            dload(cur ^ 1, kt + 1 < nk ? (kt + 1) * TBK : 0);
-#pragma unroll
-            for (int i = 4; i < 8; i++) fa[i] = rd32(ab + i * 16 * TBK);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < TFN; j++)
-                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        fa[i], fw[0][j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
-            __builtin_amdgcn_sched_barrier(0);
-            __builtin_amdgcn_s_waitcnt(0x0070);
-            __syncthreads();
-            __builtin_amdgcn_sched_barrier(0);
-            {
-                const int8_t* an = arow + (cur ^ 1) * TLDS_STAGE;
-                const int8_t* wnx = wrow + (cur ^ 1) * TLDS_STAGE;
-#pragma unroll
-                for (int j = 0; j < TFN; j++) fw[1][j] = rd32(wnx + j * 16 * TBK);
-#pragma unroll
-                for (int i = 0; i < 4; i++) fa[i] = rd32(an + i * 16 * TBK);
-            }
-#pragma unroll
-            for (int i = 4; i < 8; i++)
-#pragma unroll
-                for (int j = 0; j < TFN; j++)
-                    acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        fa[i], fw[0][j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
-#pragma unroll
-            for (int j = 0; j < TFN; j++) fw[0][j] = fw[1][j];
-        }
-    }
-
-    // epilogue: C row 4*(lane/16)+e, col lane%16 of each 16 x 16 block
-#pragma unroll
-    for (int i = 0; i < TFM; i++) {
-        float sa[4];
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int m = m0 + wm * 128 + i * 16 + q * 4 + e;
-            sa[e] = RAW ? 0.0f : (FP8 ? sA[0] : sA[m < M ? m : M - 1]);
-        }
-#pragma unroll
-        for (int j = 0; j < TFN; j++) {
-            const int n = n0 + wn * 112 + j * 16 + r16;
-            if (n >= N) continue;
-            const float swv = RAW ? 0.0f : (FP8 ? sW[0] : sW[n]);
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const int m = m0 + wm * 128 + i * 16 + q * 4 + e;
-                if (m >= M) continue;
-                if (RAW)
-                    Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
-                else
-                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sa[e] * swv);
-            }
-        }
-    }
-}
-
-// Eight-wave variant of the same tile: waves in 4 (M) x 2 (N), each 64 x 112
-// = 4 x 7 MFMA blocks (112 accumulators), two waves per SIMD, so one wave's
-// LDS latency hides behind the other's MFMAs without intra-wave prefetch.
-// Same LDS layout, swizzle, direct loads and XCD tile order as above.
+// fp8 (and the 16x16 int8 form): waves in 4 (M) x 2 (N), each 64 x 112 =
+// 4 x 7 MFMA blocks of 16 x 16 (112 accumulators), two waves per SIMD, so one
+// wave's LDS latency hides behind the other's MFMAs.
 template <bool FP8, bool RAW>
 __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ W,
@@ -366,16 +193,14 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
         const int gn = n0 + wr < N ? n0 + wr : N - 1;
         gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
     }
+    const __amdgpu_buffer_rsrc_t ra = brsrc(A), rw = brsrc(W);
     auto dload = [&](int buf, int k0) {
         int8_t* base = lds + buf * TLDS_STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
-        if (wave < 4)
-            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
+        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
+        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
     };
 
     typedef typename std::conditional<FP8, f32x4, i32x4>::type acc_t;
@@ -477,7 +302,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
 // MXFP4 x MXFP4 (E2M1 codes, one E8M0 exponent per 32 elements) on
 // v_mfma_scale_f32_16x16x128_f8f6f4, staged like k_gemm_8w: 256 x 224 tiles,
 // 8 waves of 64 x 112, K stages of 128 bytes (256 elements) global -> LDS
-// with global_load_lds_dwordx4, double buffered.  Beside each stage sit the
+// with buffer_load_dwordx4 ... lds, double buffered.  Beside each stage sit the
 // stage's 8 scale bytes of every tile row (A rows then W rows, loaded with
 // 4-byte direct loads).  Lane (r16, q) takes 16-byte chunk 4h + q of its row
 // for k-step h - exactly one 32-element block, whose exponent is the lane's
@@ -521,33 +346,32 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
     }
     // scale dwords of a stage: 2 per row x 480 rows = 15 wave instructions;
     // wave w issues instructions w and w + 8 (the latter for w < 7)
-    const int8_t* gs[2];
+    // (instruction w covers rows 32 w .. 32 w + 31: all A rows for u = 0, all
+    // W rows for u = 1)
+    uint32_t gs[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
         const int d = 64 * (wave + 8 * u) + lane, row = d >> 1, half = d & 1;
         if (row < TBM) {
             const int gr = m0 + row < M ? m0 + row : M - 1;
-            gs[u] = sA + (size_t)gr * KS + 4 * half;
+            gs[u] = (uint32_t)gr * KS + 4 * half;
         } else {
             const int r = row - TBM < TBN ? row - TBM : TBN - 1;
             const int gn = n0 + r < N ? n0 + r : N - 1;
-            gs[u] = sW + (size_t)gn * KS + 4 * half;
+            gs[u] = (uint32_t)gn * KS + 4 * half;
         }
     }
+    const __amdgpu_buffer_rsrc_t ra = brsrc(A), rw = brsrc(W), rsa = brsrc(sA), rsw = brsrc(sW);
     auto dload = [&](int buf, int kt) {
         int8_t* base = lds + buf * MXS_STAGE;
         const uint32_t k0 = (uint32_t)kt * TBK;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
-        if (wave < 4)
-            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds(gs[0] + kt * 8, base + TLDS_STAGE + wave * 256, 4, 0, 0);
-        if (wave < 7)
-            __builtin_amdgcn_global_load_lds(gs[1] + kt * 8, base + TLDS_STAGE + (wave + 8) * 256, 4, 0, 0);
+        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
+        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
+        bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs[0], kt * 8);
+        if (wave < 7) bload_lds(rsw, base + TLDS_STAGE + (wave + 8) * 256, 4, gs[1], kt * 8);
     };
 
     f32x4 acc[FM][TFN];
@@ -678,16 +502,14 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
         const int gn = n0 + wr < N ? n0 + wr : N - 1;
         gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
     }
+    const __amdgpu_buffer_rsrc_t ra = brsrc(A), rw = brsrc(W);
     auto dload = [&](int buf, int k0) {
         int8_t* base = lds + buf * TLDS_STAGE;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
-            __builtin_amdgcn_global_load_lds(A + ga[i] + k0, base + (8 * i + wave) * 1024, 16, 0, 0);
+        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
 #pragma unroll
-        for (int i = 0; i < 3; i++)
-            __builtin_amdgcn_global_load_lds(W + gw[i] + k0, base + TLDS_A + (8 * i + wave) * 1024, 16, 0, 0);
-        if (wave < 4)
-            __builtin_amdgcn_global_load_lds(W + gw[3] + k0, base + TLDS_A + (24 + wave) * 1024, 16, 0, 0);
+        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
+        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
     };
 
     typedef typename std::conditional<FP8, f32x16, i32x16>::type acc_t;
@@ -812,7 +634,6 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
 //    of tile i drains while tile i + 1 computes.
 // Barriers are raw s_barrier with explicit waits: a __syncthreads() fence
 // would also wait for the next stage's loads and the previous tile's stores.
-typedef __attribute__((address_space(3))) void* lds_ptr_t;
 constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every output buffer
 
 template <bool RAW>

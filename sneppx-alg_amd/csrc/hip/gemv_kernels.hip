@@ -31,6 +31,13 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+// Barrier for LDS hand-offs only: waits for this wave's LDS operations, not
+// for its global loads (a __syncthreads() fence would drain those too).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
 __device__ __forceinline__ u32x4 load16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
@@ -933,6 +940,269 @@ int launch_small(const W4Launch& a) {
     return launch_small_m<XPT, 4, PERM>(a);
 }
 
+// Decode GEMV for 2 <= M <= 16 activation rows: group 128, K = 1024 NC
+// (NC <= 4), on v_mfma_f32_16x16x32_bf16 with the activations as the A
+// operand (16 rows, rows >= M zero) and 16 weight rows as B.
+// Persistent: one workgroup (8 waves) per CU copies the M activation rows
+// once into LDS, then walks the 16-row groups rg = b, b + nb, ...  Wave w
+// owns columns [K w / 8, K (w + 1) / 8) of every group.  Its A fragments are
+// read from LDS once, put in the nibble unpack's column order
+// {0,4,1,5,2,6,3,7} (v_perm) and kept in registers; the 128-column sums X of
+// its activation rows come from the same fragments times a ones operand on
+// the matrix cores.  Per group each lane (row n = l % 16, quarter
+// q = l / 16) loads NC 16-byte pieces of its row (words 16 c + 4 q .. +3 of
+// the wave's part; chunk c is quantization group w NC + c); MFMA (c, e) takes
+// word e of every lane's piece c, so A and B lanes with the same quarter
+// hold the same eight columns.  Per group c:
+// y += s (sum of the 4 MFMAs) - s (128 + z) X, which removes the 128 bias of
+// the unpacked nibbles and the zero point exactly.  The 8 waves' partial
+// 16 x 16 tiles are added in LDS in wave order (deterministic).  The first
+// three groups' loads go out at the start, after every activation load of the
+// workgroup (a CU returns its loads in issue order).  PERM: qw's columns are
+// stored in the order perm (uint16 [K]); the A fragments gather
+// x[m][perm[k']] from the LDS copy.
+template <int NC, bool ZEROS, bool YF32, bool PERM>
+__global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restrict__ x,
+                                                       const uint32_t* __restrict__ qw,
+                                                       const uint16_t* __restrict__ scales,
+                                                       const uint32_t* __restrict__ qz,
+                                                       const uint16_t* __restrict__ perm,
+                                                       void* __restrict__ y, int M, int N) {
+    constexpr int K = 1024 * NC, KW = K / 8, G = K / 128, ZW = (G + 7) / 8;
+    constexpr int RS = K * 2 + 16;            // LDS row stride in bytes (16 B pad: no bank conflicts)
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    uint8_t* xs = smem;                                                  // [M][RS]
+    f32x4* red = reinterpret_cast<f32x4*>(smem + (size_t)M * RS);       // [2][8][64]
+    uint16_t* pl = reinterpret_cast<uint16_t*>(red + 2 * 8 * 64);       // PERM: [K]
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q4 = lane >> 4;
+    const int ngroups = (N + 15) >> 4, nb = gridDim.x;
+    const int kw0 = wave * NC * 16;           // first packed word of the wave's columns
+
+    // weight pieces of group rg (rows clamped into the matrix), scales (packed
+    // fp16 pairs, kept packed so nothing waits on them before use), zero words
+    // (groups wave NC .. wave NC + NC - 1 span two words only for NC = 3)
+    constexpr int NS = (NC + 1) / 2;
+    constexpr int NZ = NC == 3 ? 2 : 1;
+    // Groups past the end load the workgroup's first group again (cached, never
+    // used): every path issues the same loads, so each wait stays exact.
+    auto wload = [&](int rg, u32x4 (&wv)[NC], uint32_t (&sc)[NS], uint32_t (&zw)[NZ]) {
+        int n = (rg < ngroups ? rg : (int)blockIdx.x) * 16 + l16;
+        n = n < N ? n : N - 1;
+        const uint32_t* row = qw + (size_t)n * KW + kw0 + 4 * q4;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+            wv[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(row + 16 * c));
+        const uint16_t* srow = scales + (size_t)n * G + wave * NC;
+        if (NC % 2 == 0) {          // 4-byte aligned: G and wave NC are even
+#pragma unroll
+            for (int j = 0; j < NS; j++) sc[j] = reinterpret_cast<const uint32_t*>(srow)[j];
+        } else {
+#pragma unroll
+            for (int j = 0; j < NS; j++)
+                sc[j] = (uint32_t)srow[2 * j] | (2 * j + 1 < NC ? (uint32_t)srow[2 * j + 1] << 16 : 0u);
+        }
+#pragma unroll
+        for (int j = 0; j < NZ; j++) {
+            const int gz = (wave * NC + j * (NC - 1)) >> 3;
+            zw[j] = ZEROS ? qz[(size_t)n * ZW + gz] : 0u;
+        }
+    };
+    int rg = blockIdx.x;
+    if (rg >= ngroups) return;
+    u32x4 wa[NC], wb[NC], wc[NC];
+    uint32_t sa[NS], sb[NS], sc3[NS], za[NZ], zb[NZ], zc[NZ];
+
+    // 1. the activation rows (and perm) copied into LDS as they are
+    const int items = M * KW;
+    constexpr int XPT = (16 * KW + 511) / 512;
+    u32x4 xr[XPT];
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int it = tid + 512 * i;
+        if (it < items) xr[i] = load16(x + (size_t)it * 8);
+    }
+    constexpr int PPT = PERM ? (KW + 511) / 512 : 1;
+    u32x4 pr[PPT];
+    if (PERM) {
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int it = tid + 512 * i;
+            if (it < KW) pr[i] = load16(perm + (size_t)it * 8);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < XPT; i++) {
+        const int it = tid + 512 * i;
+        if (it < items) {
+            const int m = it / KW, w = it - m * KW;
+            *reinterpret_cast<u32x4*>(xs + (size_t)m * RS + (size_t)w * 16) = xr[i];
+        }
+    }
+    if (PERM) {
+#pragma unroll
+        for (int i = 0; i < PPT; i++) {
+            const int it = tid + 512 * i;
+            if (it < KW) *reinterpret_cast<u32x4*>(pl + (size_t)it * 8) = pr[i];
+        }
+    }
+    lds_barrier();
+    // the first three groups' weights go out once the activations are in LDS:
+    // issued earlier, a wave blocks on its weight loads (the CU's queue of
+    // outstanding loads is full) before it can stage anything
+    wload(rg, wa, sa, za);
+    wload(rg + nb, wb, sb, zb);
+    wload(rg + 2 * nb, wc, sc3, zc);
+
+    // 2. the wave's A fragments: row l16 (zero beyond M), words
+    //    kw0 + 16 c + 4 q4 + e, columns put in the order {0,4,1,5,2,6,3,7}
+    bf16x8 af[NC][4];
+    {
+        const bool mlive = l16 < M;
+        const int mrow = mlive ? l16 : 0;
+#pragma unroll
+        for (int c = 0; c < NC; c++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int wd = kw0 + 16 * c + 4 * q4 + e;
+                u32x4 v;
+                if (PERM) {      // columns perm[8 wd + j] of the original order
+                    const u32x4 pv = *reinterpret_cast<const u32x4*>(pl + (size_t)wd * 8);
+                    const uint16_t* xrow = reinterpret_cast<const uint16_t*>(xs + (size_t)mrow * RS);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        uint32_t lo = pv[j] & 0xFFFFu, hi = pv[j] >> 16;
+                        lo = lo < (uint32_t)K ? lo : (uint32_t)K - 1u;   // the caller's perm stays in LDS bounds
+                        hi = hi < (uint32_t)K ? hi : (uint32_t)K - 1u;
+                        v[j] = (uint32_t)xrow[lo] | (uint32_t)xrow[hi] << 16;
+                    }
+                } else {
+                    v = *reinterpret_cast<const u32x4*>(xs + (size_t)mrow * RS + (size_t)wd * 16);
+                }
+                u32x4 p;
+                p[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
+                p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
+                p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
+                p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
+                af[c][e] = __builtin_bit_cast(bf16x8, mlive ? p : u32x4{0u, 0u, 0u, 0u});
+            }
+    }
+    // 128-column sums of the wave's groups: rows 4 q4 + i of lane l's column
+    f32x4 xsum[NC];
+    {
+        const u32x4 ones = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};   // bf16 1.0
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[c][e], __builtin_bit_cast(bf16x8, ones), acc, 0, 0, 0);
+            xsum[c] = acc;
+        }
+    }
+
+    uint32_t nib_mask, bf_bias;
+    asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
+    asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
+
+    // 3. groups
+    int rb = 0;
+    auto group = [&](int g, u32x4 (&wv)[NC], uint32_t (&sc)[NS], uint32_t (&zw)[NZ]) {
+        f32x4 y4 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const uint32_t w = wv[c][e];
+                u32x4 b;
+                b[0] = (w & nib_mask) | bf_bias;
+                b[1] = ((w >> 4) & nib_mask) | bf_bias;
+                b[2] = ((w >> 8) & nib_mask) | bf_bias;
+                b[3] = ((w >> 12) & nib_mask) | bf_bias;
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[c][e], __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
+            }
+            const int gq = wave * NC + c;
+            const float s = f16_to_f32((uint16_t)(sc[c >> 1] >> (16 * (c & 1))));
+            const uint32_t zword = (NZ == 2 && (gq >> 3) != ((wave * NC) >> 3)) ? zw[NZ - 1] : zw[0];
+            const uint32_t z = ZEROS ? (zword >> (4 * (gq & 7))) & 15u : 8u;
+            const float cs = s * (float)(128u + z);
+#pragma unroll
+            for (int i = 0; i < 4; i++) y4[i] = fmaf(s, acc[i], fmaf(-cs, xsum[c][i], y4[i]));
+        }
+        red[(rb * 8 + wave) * 64 + lane] = y4;
+        lds_barrier();
+        if (tid < 256) {           // output (m, n) = (4 (l / 16) + i, l % 16) of lane l = tid / 4
+            const int l = tid >> 2, i = tid & 3;
+            float v = 0.0f;
+#pragma unroll
+            for (int w = 0; w < 8; w++) v += red[(rb * 8 + w) * 64 + l][i];
+            const int m = 4 * (l >> 4) + i, n = g * 16 + (l & 15);
+            if (m < M && n < N) {
+                if (YF32)
+                    reinterpret_cast<float*>(y)[(size_t)m * N + n] = v;
+                else
+                    reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = f32_to_bf16(v);
+            }
+        }
+        rb ^= 1;                   // the other reduction buffer: no second barrier
+    };
+    // up to three groups per workgroup (N <= 48 x CUs) run from the loads
+    // issued at the start, in straight-line code so each wait covers only its
+    // own group; any further groups load one at a time
+    group(rg, wa, sa, za);
+    if (rg + nb < ngroups) group(rg + nb, wb, sb, zb);
+    if (rg + 2 * nb < ngroups) group(rg + 2 * nb, wc, sc3, zc);
+    for (int g = rg + 3 * nb; g < ngroups; g += nb) {
+        wload(g, wa, sa, za);
+        group(g, wa, sa, za);
+    }
+}
+
+template <int NC, bool Z, bool F, bool PERM>
+int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
+                   const uint16_t* perm, void* y, int M, int N, size_t lds, int grid, hipStream_t st) {
+    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess &&
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
+            snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+        attr_set = true;
+    }
+    k_w4a16_gemv_mt<NC, Z, F, PERM><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, M, N);
+    return snx_launch_check("k_w4a16_gemv_mt");
+}
+
+template <int NC, bool PERM>
+int launch_gemv_mt_nc(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
+                      const uint16_t* perm, void* y, int y_f32, int M, int N, size_t lds, int grid,
+                      hipStream_t st) {
+    if (qz) {
+        if (y_f32) return launch_gemv_mt<NC, true, true, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+        return launch_gemv_mt<NC, true, false, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+    }
+    if (y_f32) return launch_gemv_mt<NC, false, true, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+    return launch_gemv_mt<NC, false, false, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+}
+
+template <bool PERM>
+int launch_gemv_mt_k(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
+                     const uint16_t* perm, void* y, int y_f32, int M, int N, int K, size_t lds, int grid,
+                     hipStream_t st) {
+    switch (K / 1024) {
+        case 1: return launch_gemv_mt_nc<1, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
+        case 2: return launch_gemv_mt_nc<2, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
+        case 3: return launch_gemv_mt_nc<3, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
+        default: return launch_gemv_mt_nc<4, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
+    }
+}
+
 // Generic W4A16: one wave per output column n, any group layout and M.
 __global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restrict__ x,
                                                        const uint32_t* __restrict__ qw,
@@ -1132,6 +1402,39 @@ int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scal
     if (M <= 32)
         return launch_w4a16<2>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
     return launch_w4a16<4>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+}
+
+size_t snx_w4a16_mt_lds(size_t M, size_t K, int perm) {
+    return M * (K * 2 + 16) + 2 * 8 * 64 * 16 + (perm ? K * 2 : 0);
+}
+
+int snx_w4a16_mt_ok(size_t M, size_t K, int group, int perm) {
+    return M >= 2 && M <= 16 && group == 128 && K % 1024 == 0 && K >= 1024 && K <= 4096 &&
+           snx_w4a16_mt_lds(M, K, perm) <= 160 * 1024;
+}
+
+int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                        const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
+                        size_t N, size_t K, void* st) {
+    if (!snx_w4a16_mt_ok(M, K, 128, perm != NULL)) {
+        snx_set_error("w4a16 gemv: M=%zu K=%zu outside the small-M kernel", M, K);
+        return -1;
+    }
+    static int ncu = 0;
+    if (ncu == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+    }
+    const size_t ngroups = (N + 15) / 16;
+    const int grid = (int)(ngroups < (size_t)ncu ? ngroups : (size_t)ncu);
+    const size_t lds = snx_w4a16_mt_lds(M, K, perm != NULL);
+    if (perm)
+        return launch_gemv_mt_k<true>(x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, lds,
+                                      grid, S(st));
+    return launch_gemv_mt_k<false>(x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, lds, grid,
+                                   S(st));
 }
 
 int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,

@@ -147,6 +147,11 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
                                        Mp, stream);
         return rc;
     }
+    if (!g_idx && snx_w4a16_mt_ok(M, K, group, 0) && aligned16(x) && aligned16(qweight) &&
+        ((uintptr_t)scales & 3u) == 0 && ((uintptr_t)qzeros & 3u) == 0) {
+        /* 2 <= M <= 16: one persistent workgroup per CU, activations staged once */
+        return snx_k_w4a16_gemv_mt(x, qweight, scales, qzeros, NULL, y, y_f32, M, N, K, stream);
+    }
     const int kspan = snx_w4a16_splitk_span(M, K, group);
     if (!g_idx && M > 4 && kspan && aligned16(x) && aligned16(qweight)) {
         /* 5 <= M <= 16: split-K decode + ordered reduction of the partials */
@@ -224,6 +229,10 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
     REQUIRE(group > 0 && K % (size_t)group == 0,
             "qlinear_w4a16_actorder: group %d must divide K=%zu", group, K);
     snx_clear_error();
+    if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) && ((uintptr_t)scales & 3u) == 0 &&
+        ((uintptr_t)qzeros & 3u) == 0 && snx_w4a16_mt_ok(M, K, group, 1))
+        return snx_k_w4a16_gemv_mt(x, qweight_sorted, scales, qzeros, perm, y, y_dtype == SNEPPX_FLOAT32,
+                                   M, N, K, stream);
     if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) &&
         snx_w4a16_small_ok(M, K, group, 1))
         return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y,

@@ -126,6 +126,13 @@ int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, siz
 int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs, size_t N,
                           size_t K, void* stream);
 /* any group size / g_idx, any M: reference-layout fallback */
+/* 2 <= M <= 16 decode GEMV (group 128, K = 1024 .. 4096 in steps of 1024): one
+ * persistent workgroup per CU; perm != NULL gathers x[m][perm[k]] (M <= 8). */
+size_t snx_w4a16_mt_lds(size_t M, size_t K, int perm);
+int snx_w4a16_mt_ok(size_t M, size_t K, int group, int perm);
+int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                        const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
+                        size_t N, size_t K, void* stream);
 int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
                         int y_f32, size_t M, size_t N, size_t K, int group, void* stream);

@@ -200,6 +200,27 @@ def test_w4a16_gemv_m1_group128(lib, oracle, N, K, sym, out):
     assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
 
 
+@pytest.mark.parametrize("M,N,K,sym,out", [
+    (2, 8197, 1024, False, "f32"), (3, 45, 2048, True, "bf16"), (5, 4099, 3072, False, "f32"),
+    (8, 11008, 4096, True, "f32"), (16, 300, 4096, False, "bf16"), (16, 9000, 2048, True, "f32"),
+    (7, 17, 4096, False, "f32")])
+def test_w4a16_gemv_small_m_persistent(lib, oracle, M, N, K, sym, out):
+    # the persistent 2 <= M <= 16 kernel: every K it takes (1024 .. 4096),
+    # more row groups than workgroups (three per workgroup at N = 8197, 9000,
+    # 11008), fewer (N = 17, 45), N not a multiple of 16, with and without
+    # zero points, fp32 and bf16 outputs
+    group = 128
+    print(f"[gpu] w4a16 small-M M={M} N={N} K={K} sym={sym} out={out}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, 90 + M + K, sym=sym)
+    x = bf16_bits(np.random.default_rng(100 + M).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), None if qz is None else to_dev(qz), None, G, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
 def test_w4a16_gemv_symmetric_and_tails(lib, oracle):
     # symmetric zero 8 (no qzeros), N not a multiple of 16, K of 1024
     N, K, group, M = 45, 1024, 256, 3
@@ -260,7 +281,8 @@ def test_actorder_prepare_rejects_uneven_groups(lib, oracle):
 @pytest.mark.parametrize("M,ydt,K", [(1, torch.float32, 4096), (1, torch.bfloat16, 4096),
                                      (1, torch.float32, 8192), (1, torch.float32, 2048),
                                      (3, torch.float32, 4096), (4, torch.bfloat16, 4096),
-                                     (8, torch.float32, 4096), (300, torch.float32, 4096)])
+                                     (8, torch.float32, 4096), (300, torch.float32, 4096),
+                                     (2, torch.bfloat16, 2048), (16, torch.float32, 1024)])
 def test_w4a16_actorder_prepared(lib, oracle, M, ydt, K):
     """Prepared (group-contiguous) weights give the layer's result on the
     original column order: compared with the oracle on qweight + g_idx."""
@@ -281,7 +303,7 @@ def test_w4a16_actorder_prepared(lib, oracle, M, ydt, K):
 
 
 @pytest.mark.parametrize("M,N,K,group,sym,out", [
-    (5, 11008, 4096, 128, False, "f32"),     # split-K decode, 4 spans of 1024
+    (5, 11008, 4096, 128, False, "f32"),     # persistent small-M kernel (group 128, K <= 4096)
     (8, 1000, 1408, 128, True, "f32"),       # 11 steps: spans of 128, N tail
     (12, 64, 4096, 256, False, "bf16"),      # one row block, group 256
     (16, 4096, 14336, 128, False, "f32"),    # down-projection width
