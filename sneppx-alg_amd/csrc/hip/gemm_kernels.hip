@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "codec.h"
+#include "launch.h"
 #include "../snx_internal.h"
 
 using namespace snx;
@@ -448,14 +449,11 @@ int launch_mxfp4_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, con
                        void* out, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const size_t lds = 2 * (size_t)MXS_STAGE;
-    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            snx_set_error("mxfp4 gemm: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("mxfp4 gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     k_mxfp4_tiled<YF32><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
     return snx_launch_check("k_mxfp4_tiled");
@@ -816,25 +814,16 @@ int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* s
                uint16_t* out, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const int ntiles = tiles_m * tiles_n;
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-            ncu = 256;
-    }
+    const int ncu = snx::cu_count();
     // one workgroup per CU (rounded down to a multiple of 8: tiles keep their XCD)
     int grid = ncu >= 8 ? ncu - ncu % 8 : ncu;
     if (grid > ntiles) grid = ntiles;
     const size_t lds = 2 * (size_t)TLDS_STAGE;
-    static bool attr_set = false;
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_i8p<RAW>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_i8p<RAW>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     k_gemm_i8p<RAW><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K, tiles_m, tiles_n);
     return snx_launch_check("k_gemm_i8p");
@@ -849,14 +838,11 @@ int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* s
         return -1;
     }
     const size_t lds = 2 * (size_t)TLDS_STAGE;
-    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_x32<FP8, RAW>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_x32<FP8, RAW>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     k_gemm_x32<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
                                                           tiles_m, tiles_n);
@@ -872,14 +858,11 @@ int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float*
         return -1;
     }
     const size_t lds = 2 * (size_t)TLDS_STAGE;
-    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_gemm_8w<FP8, RAW>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8w<FP8, RAW>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     k_gemm_8w<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
                                                             tiles_m, tiles_n);

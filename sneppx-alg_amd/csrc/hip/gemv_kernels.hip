@@ -14,6 +14,7 @@
 #include <cstdint>
 
 #include "codec.h"
+#include "launch.h"
 #include "../snx_internal.h"
 
 using namespace snx;
@@ -1164,16 +1165,12 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
 template <int NC, bool Z, bool F, bool PERM>
 int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
                    const uint16_t* perm, void* y, int M, int N, size_t lds, int grid, hipStream_t st) {
-    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess &&
-            hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) != hipSuccess) {
-            snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    // the LDS size depends on M: opt in to the most any call may ask for
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>);
+    if (snx::lds_optin(kfn, 160 * 1024, lds_done) != hipSuccess) {
+        snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     k_w4a16_gemv_mt<NC, Z, F, PERM><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, M, N);
     return snx_launch_check("k_w4a16_gemv_mt");
@@ -1420,13 +1417,7 @@ int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* s
         snx_set_error("w4a16 gemv: M=%zu K=%zu outside the small-M kernel", M, K);
         return -1;
     }
-    static int ncu = 0;
-    if (ncu == 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
-            ncu = 256;
-    }
+    const int ncu = snx::cu_count();
     const size_t ngroups = (N + 15) / 16;
     const int grid = (int)(ngroups < (size_t)ncu ? ngroups : (size_t)ncu);
     const size_t lds = snx_w4a16_mt_lds(M, K, perm != NULL);

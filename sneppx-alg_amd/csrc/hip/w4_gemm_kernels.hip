@@ -25,6 +25,7 @@
 #include <cstdint>
 
 #include "codec.h"
+#include "launch.h"
 #include "../snx_internal.h"
 
 using namespace snx;
@@ -335,14 +336,11 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                    int group, int Mp, hipStream_t st) {
     const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
     const size_t lds = (size_t)GSTAGES * GRING;
-    static bool attr_set = false;   // one-time opt-in to > 64 KB of LDS per workgroup
-    if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN>),
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-            snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
-            return -1;
-        }
-        attr_set = true;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
     }
     const int gshift = __builtin_ctz((unsigned)group);
     k_w4a16_gemm<ZEROS, YF32, WN><<<tiles_m * tiles_n, 512, lds, st>>>(
