@@ -132,6 +132,10 @@ __global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
         it = it < NIT ? it : NIT - 1;
         xr[i] = reinterpret_cast<const float4*>(x)[it];
     }
+    // every wave's activation loads go out before any weight load of the
+    // workgroup: a CU returns its loads in issue order
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     u32x4 w[SL];
 #pragma unroll
