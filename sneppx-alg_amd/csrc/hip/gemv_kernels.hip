@@ -898,7 +898,7 @@ int launch_small_m(const W4Launch& a) {
     return launch_small_vs<XPT, MM, false, PERM>(a);
 }
 
-// k_w4a16_gemv1 applies: M = 1, group 128, K = 2048 T (T <= 4), 16-byte aligned scales.
+// k_w4a16_gemv1 applies: M = 1, group 128, K = 2048 T (T <= 8), 16-byte aligned scales.
 size_t gemv1_lds(size_t K, bool perm) {
     const size_t nch = K / 32, g = K / 128;
     return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
@@ -908,6 +908,18 @@ template <int T, bool PERM>
 int launch_gemv1_t(const W4Launch& a) {
     dim3 grid((unsigned)((a.N + 15) / 16)), block(512);
     const size_t lds = gemv1_lds((size_t)a.K, PERM);
+    if (lds > 64 * 1024) {   // PERM at K > 8192: the staged copies of x and perm
+        static std::atomic<uint64_t> lds_done[4];   // (zeros, f32 out) variants, per device
+        const void* kfn[4] = {reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, false, PERM>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, true, PERM>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, false, PERM>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, true, PERM>)};
+        const int v = (a.qz ? 2 : 0) + (a.y_f32 ? 1 : 0);
+        if (snx::lds_optin(kfn[v], (int)lds, lds_done[v]) != hipSuccess) {
+            snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+    }
 #define SNX_G1(Z, F)                                                                      \
     k_w4a16_gemv1<T, Z, F, PERM><<<grid, block, lds, a.s>>>(a.x, a.qw, a.scales, a.qz, a.perm, \
                                                             a.y, a.N)
@@ -923,7 +935,7 @@ int launch_gemv1_t(const W4Launch& a) {
 }
 
 bool gemv1_ok(const W4Launch& a) {
-    return a.M == 1 && a.group == 128 && a.K % 2048 == 0 && a.K <= 8192 &&
+    return a.M == 1 && a.group == 128 && a.K % 2048 == 0 && a.K <= 16384 &&
            ((uintptr_t)a.scales & 15u) == 0 && ((uintptr_t)a.qz & 3u) == 0;
 }
 
@@ -933,7 +945,11 @@ int launch_gemv1(const W4Launch& a) {
         case 1: return launch_gemv1_t<1, PERM>(a);
         case 2: return launch_gemv1_t<2, PERM>(a);
         case 3: return launch_gemv1_t<3, PERM>(a);
-        default: return launch_gemv1_t<4, PERM>(a);
+        case 4: return launch_gemv1_t<4, PERM>(a);
+        case 5: return launch_gemv1_t<5, PERM>(a);
+        case 6: return launch_gemv1_t<6, PERM>(a);
+        case 7: return launch_gemv1_t<7, PERM>(a);
+        default: return launch_gemv1_t<8, PERM>(a);
     }
 }
 

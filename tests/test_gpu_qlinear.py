@@ -183,9 +183,11 @@ def test_w4a16_gemv_shapes(lib, oracle, M, N, K):
 
 @pytest.mark.parametrize("N,K,sym,out", [
     (1, 2048, False, "f32"), (17, 4096, True, "bf16"), (1001, 6144, False, "f32"),
-    (300, 8192, True, "f32"), (16, 8192, False, "bf16"), (11008, 2048, False, "f32")])
+    (300, 8192, True, "f32"), (16, 8192, False, "bf16"), (11008, 2048, False, "f32"),
+    (4096, 14336, False, "f32"), (33, 10240, True, "bf16"), (250, 12288, False, "bf16"),
+    (19, 16384, True, "f32")])
 def test_w4a16_gemv_m1_group128(lib, oracle, N, K, sym, out):
-    # the M = 1, group-128 decode kernel at every K it takes (2048 T, T <= 4),
+    # the M = 1, group-128 decode kernel at every K it takes (2048 T, T <= 8),
     # row counts that leave part of the last workgroup empty, with and
     # without zero points, fp32 and bf16 outputs
     group = 128
@@ -282,7 +284,8 @@ def test_actorder_prepare_rejects_uneven_groups(lib, oracle):
                                      (1, torch.float32, 8192), (1, torch.float32, 2048),
                                      (3, torch.float32, 4096), (4, torch.bfloat16, 4096),
                                      (8, torch.float32, 4096), (300, torch.float32, 4096),
-                                     (2, torch.bfloat16, 2048), (16, torch.float32, 1024)])
+                                     (2, torch.bfloat16, 2048), (16, torch.float32, 1024),
+                                     (1, torch.float32, 14336), (1, torch.bfloat16, 16384)])
 def test_w4a16_actorder_prepared(lib, oracle, M, ydt, K):
     """Prepared (group-contiguous) weights give the layer's result on the
     original column order: compared with the oracle on qweight + g_idx."""
