@@ -153,8 +153,10 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         return snx_k_w4a16_gemv_mt(x, qweight, scales, qzeros, NULL, y, y_f32, M, N, K, stream);
     }
     const int kspan = snx_w4a16_splitk_span(M, K, group);
-    if (!g_idx && M > 4 && kspan && aligned16(x) && aligned16(qweight)) {
-        /* 5 <= M <= 16: split-K decode + ordered reduction of the partials */
+    if (!g_idx && (M > 4 || (M > 1 && !snx_w4a16_small_ok(M, K, group, 0))) && kspan &&
+        aligned16(x) && aligned16(qweight)) {
+        /* 5 <= M <= 16, and 2 <= M <= 4 where the LDS-staged small-M kernel does
+         * not apply (large K): split-K decode + ordered reduction of the partials */
         const size_t S = K / (size_t)kspan;
         float* part = (float*)snx_workspace(S * M * N * sizeof(float), 1, stream);
         if (!part) return -1;

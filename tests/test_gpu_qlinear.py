@@ -310,6 +310,9 @@ def test_w4a16_actorder_prepared(lib, oracle, M, ydt, K):
     (8, 1000, 1408, 128, True, "f32"),       # 11 steps: spans of 128, N tail
     (12, 64, 4096, 256, False, "bf16"),      # one row block, group 256
     (16, 4096, 14336, 128, False, "f32"),    # down-projection width
+    (2, 4096, 14336, 128, True, "bf16"),     # M <= 4 beyond the LDS-staged small-M kernel
+    (3, 77, 14336, 128, False, "f32"),
+    (4, 1000, 6144, 256, False, "f32"),
 ])
 def test_w4a16_splitk_decode(lib, oracle, M, N, K, group, sym, out):
     print(f"[gpu] w4a16 split-K M={M} N={N} K={K} g={group} sym={sym} out={out}", flush=True)
