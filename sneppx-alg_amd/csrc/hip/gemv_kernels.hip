@@ -1306,6 +1306,23 @@ __global__ void __launch_bounds__(256) k_w4_permute_cols(const uint32_t* __restr
     qs[i] = out;
 }
 
+// k_w8_gemv1 at K = 1024 SL: the activations staged in LDS (SL * 5 KB; above
+// 64 KB from SL = 13 on, which needs the one-time opt-in)
+template <int SL>
+int launch_w8_gemv1(const float* x, const int8_t* q, const float* s, float* y, size_t N,
+                    hipStream_t st) {
+    const size_t lds = (size_t)SL * 64 * 20 * sizeof(float) + 16 * sizeof(float);
+    if (lds > 64 * 1024) {
+        static std::atomic<uint64_t> lds_done{0};
+        if (snx::lds_optin(reinterpret_cast<const void*>(&k_w8_gemv1<SL>), (int)lds, lds_done) != hipSuccess) {
+            snx_set_error("w8 gemv: cannot reserve %zu bytes of LDS", lds);
+            return -1;
+        }
+    }
+    k_w8_gemv1<SL><<<(unsigned)((N + 15) / 16), 1024, lds, st>>>(x, q, s, y, (int)N);
+    return snx_launch_check("k_w8_gemv1");
+}
+
 }  // namespace
 
 extern "C" {
@@ -1356,14 +1373,25 @@ int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs
 
 int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
                   size_t K, void* st) {
-    if (M == 1 && (K == 1024 || K == 2048 || K == 4096 || K == 8192)) {
-        const size_t lds = (K / 1024) * 64 * 20 * sizeof(float) + 16 * sizeof(float);
-        const unsigned grid = (unsigned)((N + 15) / 16);
-        if (K == 1024) k_w8_gemv1<1><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
-        else if (K == 2048) k_w8_gemv1<2><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
-        else if (K == 4096) k_w8_gemv1<4><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
-        else k_w8_gemv1<8><<<grid, 1024, lds, S(st)>>>(x, q, s, y, (int)N);
-        return snx_launch_check("k_w8_gemv1");
+    if (M == 1 && K % 1024 == 0 && K <= 16384) {
+        switch (K / 1024) {
+            case 1: return launch_w8_gemv1<1>(x, q, s, y, N, S(st));
+            case 2: return launch_w8_gemv1<2>(x, q, s, y, N, S(st));
+            case 3: return launch_w8_gemv1<3>(x, q, s, y, N, S(st));
+            case 4: return launch_w8_gemv1<4>(x, q, s, y, N, S(st));
+            case 5: return launch_w8_gemv1<5>(x, q, s, y, N, S(st));
+            case 6: return launch_w8_gemv1<6>(x, q, s, y, N, S(st));
+            case 7: return launch_w8_gemv1<7>(x, q, s, y, N, S(st));
+            case 8: return launch_w8_gemv1<8>(x, q, s, y, N, S(st));
+            case 9: return launch_w8_gemv1<9>(x, q, s, y, N, S(st));
+            case 10: return launch_w8_gemv1<10>(x, q, s, y, N, S(st));
+            case 11: return launch_w8_gemv1<11>(x, q, s, y, N, S(st));
+            case 12: return launch_w8_gemv1<12>(x, q, s, y, N, S(st));
+            case 13: return launch_w8_gemv1<13>(x, q, s, y, N, S(st));
+            case 14: return launch_w8_gemv1<14>(x, q, s, y, N, S(st));
+            case 15: return launch_w8_gemv1<15>(x, q, s, y, N, S(st));
+            default: return launch_w8_gemv1<16>(x, q, s, y, N, S(st));
+        }
     }
     if (K % 16 == 0) {
         constexpr int R = 4;

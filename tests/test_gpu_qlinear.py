@@ -125,7 +125,8 @@ def test_dev_fp8_scaled_bit_exact(lib, oracle, n):
 
 # ---------------------------------------------------------------- linears
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 1000, 4096), (2, 37, 100), (1, 17, 1024),
-                                   (1, 1001, 2048), (1, 300, 8192), (1, 1, 4096)])
+                                   (1, 1001, 2048), (1, 300, 8192), (1, 1, 4096), (1, 4096, 14336),
+                                   (1, 33, 3072), (1, 100, 16384)])
 def test_w8_gemv(lib, oracle, M, N, K):
     print(f"[gpu] w8 gemv M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M * N + K)
