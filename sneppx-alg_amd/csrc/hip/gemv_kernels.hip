@@ -1415,6 +1415,16 @@ size_t snx_w4a16_small_lds(size_t M, size_t K, int perm) {
 }
 
 // The LDS-staged kernel: M <= 4, power-of-two groups, at most 8 items/thread.
+int snx_w4a16_gemv1_ok(size_t M, size_t K, int group, const void* scales, const void* qzeros) {
+    W4Launch a{};
+    a.M = (int)M;
+    a.K = (int)K;
+    a.group = group;
+    a.scales = static_cast<const uint16_t*>(scales);
+    a.qz = static_cast<const uint32_t*>(qzeros);
+    return K <= 16384 && gemv1_ok(a);
+}
+
 int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
     return M >= 1 && M <= 4 && K % 512 == 0 && group >= 128 && (group & (group - 1)) == 0 &&
            K % (size_t)group == 0 && snx_w4a16_small_lds(M, K, perm) <= 65536 &&
@@ -1427,8 +1437,9 @@ int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scal
     const int G = (int)(K / (size_t)group);
     const size_t lds = snx_w4a16_small_lds(M, K, perm != NULL);
     const size_t items = M * (K / 8);
+    W4Launch a{x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, G, group, lds, S(st)};
+    if (gemv1_ok(a)) return perm ? launch_gemv1<true>(a) : launch_gemv1<false>(a);
     if (snx_w4a16_small_ok(M, K, group, perm != NULL)) {
-        W4Launch a{x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, G, group, lds, S(st)};
         if (perm) {
             if (items <= 2 * 256) return launch_small<2, true>(a);
             if (items <= 4 * 256) return launch_small<4, true>(a);

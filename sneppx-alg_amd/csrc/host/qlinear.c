@@ -236,7 +236,7 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
         return snx_k_w4a16_gemv_mt(x, qweight_sorted, scales, qzeros, perm, y, y_dtype == SNEPPX_FLOAT32,
                                    M, N, K, stream);
     if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) &&
-        snx_w4a16_small_ok(M, K, group, 1))
+        (snx_w4a16_small_ok(M, K, group, 1) || snx_w4a16_gemv1_ok(M, K, group, scales, qzeros)))
         return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y,
                                 y_dtype == SNEPPX_FLOAT32, M, N, K, group, stream);
     /* other shapes: gather the activation columns once, then the plain path */
