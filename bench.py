@@ -168,7 +168,7 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = timer.stream
-    calls = [bound(lib, "SNEPPX_qlinear_w4a16", x, c[0], c[1], c[2], None, G, y, SNEPPX_BFLOAT16,
+    calls = [bound(lib, "SNEPPX_qlinear_w4a16", x, c[0], c[1], c[2], None, G, None, y, SNEPPX_BFLOAT16,
                    M, N, K, group, C.c_void_p(st)) for c in ws]
     qwa, sca, qza = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws]), ptr_array([c[2] for c in ws])
     loop = make_loop("snxb_loop_w4a16", C.c_int(len(ws)), x, qwa, sca, qza, y, C.c_int(SNEPPX_BFLOAT16),
@@ -198,20 +198,22 @@ def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
     qs = torch.empty_like(qw)
     order = torch.empty(K, dtype=torch.int16, device="cuda")
     lib.qlinear_w4_actorder_prepare(qw, g_idx, G, qs, order)
+    host = {"qw": _u32(qw), "sc": _u16(sc), "g_idx": g_idx.cpu().numpy()}
     del qw
     ws = [(qs.clone(), sc.clone()) for _ in range(copies)]
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
     y = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = timer.stream
-    calls = [bound(lib, "SNEPPX_qlinear_w4a16_actorder", x, c[0], c[1], None, order, y,
+    calls = [bound(lib, "SNEPPX_qlinear_w4a16_actorder", x, c[0], c[1], None, order, None, y,
                    SNEPPX_BFLOAT16, M, N, K, 128, C.c_void_p(st)) for c in ws]
     qwa, sca = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws])
     loop = make_loop("snxb_loop_w4a16_actorder", C.c_int(len(ws)), x, qwa, sca, order, y,
                      C.c_int(SNEPPX_BFLOAT16), M, N, K, C.c_int(128), C.c_void_p(st))
     total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
     nbytes = w4_bytes(M, N, K, G, zeros=False) + K * 2      # + uint16 perm
+    host["x"] = _u16(x)
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
-            "gbs_kernel": nbytes / mean_launch / 1e6}
+            "gbs_kernel": nbytes / mean_launch / 1e6, "host": host}
 
 
 def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
@@ -231,13 +233,16 @@ def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
     x = torch.randn((1, K), device="cuda", generator=g)
     y = torch.empty((1, N), device="cuda")
     st = timer.stream
-    calls = [bound(lib, "SNEPPX_qlinear_w8_gemv", x, c[0], c[1], y, 1, N, K, C.c_void_p(st)) for c in ws]
+    calls = [bound(lib, "SNEPPX_qlinear_w8_gemv", x, c[0], c[1], None, y, 1, N, K, C.c_void_p(st))
+             for c in ws]
     loop = make_loop("snxb_loop_w8_gemv", C.c_int(len(ws)), x, ptr_array([c[0] for c in ws]),
                      ptr_array([c[1] for c in ws]), y, 1, N, K, C.c_void_p(st))
     total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
     nbytes = N * K + N * 4 + K * 4 + N * 4
+    host = {"q": q.cpu().numpy(), "s": s.cpu().numpy(), "x": x.cpu().numpy()}
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
-            "gbs_kernel": nbytes / mean_launch / 1e6, "codes_differing_half_even": mismatch}
+            "gbs_kernel": nbytes / mean_launch / 1e6, "codes_differing_half_even": mismatch,
+            "host": host}
 
 
 def bench_host_api(lib, N, K, reps=5):
@@ -279,8 +284,10 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
     del a32, w32
     total, mean_launch, _ = timer.run(calls, steps, warmup)
     ops = 2 * M * N * K
+    host = {"A": A[:CPU_ROWS].cpu().numpy(), "W": W.cpu().numpy(), "sA": sA[:CPU_ROWS].cpu().numpy(),
+            "sW": sW.cpu().numpy(), "M": M}
     return {"ops": ops, "ms_per_step": total / steps, "tops": ops / (total / steps) / 1e9,
-            "tops_kernel": ops / mean_launch / 1e9}
+            "tops_kernel": ops / mean_launch / 1e9, "host": host}
 
 
 def bench_mxfp4(lib, timer, torch, M, N, K, steps, warmup):
@@ -389,8 +396,103 @@ def bench_chain(lib, timer, torch, steps, warmup):
         N, K = shapes[name]
         per[name] = {"us": round(t / steps * 1e3, 1), "tflops": round(2 * T * N * K / (t / steps) / 1e9, 1)}
     flops = 2 * T * sum(N * K for N, K in shapes.values())
+    host = {"x": _u16(x[:2 * CPU_ROWS]), "attn": _u16(attn[:2 * CPU_ROWS]), "shapes": shapes,
+            "w": {name: (_u32(qw), _u16(sc), _u32(qz)) for name, (qw, sc, qz, G) in ws.items()}}
     return {"T": T, "chunk_lens": lens, "flops": flops, "ms_per_step": total / steps,
-            "tflops": flops / (total / steps) / 1e9, "per_linear": per}
+            "tflops": flops / (total / steps) / 1e9, "per_linear": per, "host": host}
+
+
+CPU_ROWS = 16     # activation rows of the C4 / C5 CPU slices
+
+
+def _u32(t):
+    import numpy as np
+    return t.cpu().numpy().view(np.uint32)
+
+
+def _u16(t):
+    import numpy as np
+    import torch
+    return t.cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def _per_call(fn, seconds, max_reps=200):
+    """Seconds per call of fn(), repeated for about `seconds` (at least once)."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or reps >= max_reps:
+            return el / reps, reps, el
+
+
+def _cpu_entry(value, unit, sample, kind="port"):
+    return {"value": value, "unit": unit, "cores": 1, "kind": kind, "sample": sample,
+            "build": "oracle/liboracle_perf.so (-O3 -march=x86-64-v3), one thread"}
+
+
+def cpu_legs(orc, jobs, seconds):
+    """The oracle's C restatement of the reference CPU path for every extra
+    config (dequantise, then the k-ascending fp32 dot of tensor.c:1820-1823),
+    one host thread; each job fills the `cpu_baseline` of its extra entry."""
+    import numpy as np
+    for entry, kind, h in jobs:
+        if kind == "w8":                       # C1, full shape
+            per, reps, el = _per_call(lambda: orc.w8_linear(h["x"], h["q"], h["s"]), seconds)
+            N, K = h["q"].shape
+            nbytes = N * K + N * 4 + K * 4 + N * 4
+            entry["cpu_baseline"] = _cpu_entry(round(nbytes / per / 1e9, 3), "GB/s",
+                                               f"full C1 shape, {reps} calls in {el:.1f} s ({per * 1e3:.2f} ms/call)")
+        elif kind in ("w4", "w4_gidx"):         # C2 / C3, full shape
+            N = h["qw"].shape[0]
+            K = h["qw"].shape[1] * 8
+            gi = h.get("g_idx")
+            per, reps, el = _per_call(lambda: orc.w4a16_linear(h["x"], h["qw"], h["sc"], h.get("qz"), gi,
+                                                               N, K, 128), seconds)
+            entry["cpu_baseline"] = _cpu_entry(round(h["bytes"] / per / 1e9, 4), "GB/s",
+                                               f"full shape M={h['x'].shape[0]}, {reps} calls in {el:.1f} s "
+                                               f"({per * 1e3:.1f} ms/call)")
+        elif kind in ("i8", "fp8"):            # C4: rows of A, extrapolated to M
+            A, W, M = h["A"], h["W"], h["M"]
+            N, K = W.shape
+            if kind == "i8":
+                a_deq = (A.astype(np.float32) * h["sA"][:, None]).astype(np.float32)   # (float)q * s
+                fn = lambda: orc.w8_linear(a_deq, W, h["sW"])                          # noqa: E731
+            else:
+                fn = lambda: orc.fp8_gemm(A, W, np.float32(h["sA"][0]), np.float32(h["sW"][0]))  # noqa: E731
+            per, reps, el = _per_call(fn, seconds, max_reps=3)
+            full = per * M / A.shape[0]
+            entry["cpu_baseline"] = _cpu_entry(round(2 * M * N * K / full / 1e12, 6), "TOPS",
+                                               f"{A.shape[0]} of {M} rows of A against all of W, "
+                                               f"{per:.2f} s per slice, extrapolated linearly to M={M} "
+                                               f"({full:.0f} s per call)")
+        elif kind == "chain":                  # C5: token slices, extrapolated to T
+            shapes, w = h["shapes"], h["w"]
+
+            def layer(rows):
+                xs, at = h["x"][:rows], h["attn"][:rows]
+                for name, inp in (("qkv", xs), ("o", at)):
+                    N, K = shapes[name]
+                    orc.w4a16_linear(inp, *w[name], None, N, K, 128)
+                N, K = shapes["gate_up"]
+                rc, gu = orc.w4a16_linear(at, *w["gate_up"], None, N, K, 128)
+                F = N // 2
+                g = gu[:, :F]
+                with np.errstate(over="ignore"):
+                    act = (g / (np.float32(1) + np.exp(-g)) * gu[:, F:]).astype(np.float32)
+                ab = act.view(np.uint32)
+                ab = ((ab + 0x7FFF + ((ab >> 16) & 1)) >> 16).astype(np.uint16)   # bf16, as the GPU chain
+                N, K = shapes["down"]
+                orc.w4a16_linear(ab, *w["down"], None, N, K, 128)
+            lo, hi = CPU_ROWS // 2, CPU_ROWS
+            t_lo, _, _ = _per_call(lambda: layer(lo), 0.0, max_reps=1)
+            t_hi, _, _ = _per_call(lambda: layer(hi), 0.0, max_reps=1)
+            T = h["T"]
+            full = t_lo + (T - lo) * (t_hi - t_lo) / (hi - lo)
+            entry["cpu_baseline"] = _cpu_entry(round(h["flops"] / full / 1e12, 6), "TFLOP/s",
+                                               f"the layer on {lo} and {hi} tokens ({t_lo:.2f} / {t_hi:.2f} s), "
+                                               f"extrapolated linearly to T={T} ({full:.0f} s per layer)")
 
 
 def cpu_baseline(ws_host, x_host, N, K, group, seconds):
@@ -514,24 +616,30 @@ def main():
     print(f"[bench] C2 M=1: {head['gbs']:.0f} GB/s whole-job, kernel {head['launch_ms_mean'] * 1e3:.2f} us",
           file=sys.stderr, flush=True)
 
-    extra = []
+    extra, cpu_jobs = [], []
     if not args.no_extra:
         for m in (4, 16):
-            r, _ = bench_w4a16(lib, timer, torch, m, N, K, group, args.copies, max(50, args.steps // 4), 10)
+            r, (ws_m, x_m, _, _) = bench_w4a16(lib, timer, torch, m, N, K, group, args.copies,
+                                               max(50, args.steps // 4), 10)
             extra.append({"workload": f"C2 W4A16 g128 GEMV N={N} K={K} M={m}", "value": round(r["gbs"], 1),
                           "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                           "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
+            cpu_jobs.append((extra[-1], "w4", {"qw": _u32(ws_m[0][0]), "sc": _u16(ws_m[0][1]),
+                                               "qz": _u32(ws_m[0][2]), "x": _u16(x_m), "bytes": r["bytes"]}))
+            del ws_m, x_m
         for m in (1, 8):
             r = bench_w4a16_gptq(lib, timer, torch, m, N, K, args.copies, max(50, args.steps // 4), 10)
             extra.append({"workload": f"C3 GPTQ act-order W4A16 (prepared) N={N} K={K} M={m}",
                           "value": round(r["gbs"], 1), "unit": "GB/s",
                           "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                           "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
+            cpu_jobs.append((extra[-1], "w4_gidx", dict(r["host"], bytes=r["bytes"])))
         r = bench_w8(lib, timer, torch, 4096, 4096, 20, max(50, args.steps // 4), 10)
         extra.append({"workload": "C1 W8 weight-only GEMV N=4096 K=4096 M=1 fp32", "value": round(r["gbs"], 1),
                       "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                       "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
                       "codes_differing_half_even": r["codes_differing_half_even"]})
+        cpu_jobs.append((extra[-1], "w8", r["host"]))
         h = bench_host_api(lib, 4096, 4096)
         extra.append({"workload": "host API SNEPPX_quantize_int8_channel 4096x4096 (host buffers, PCIe included)",
                       "value": round(h["ms_per_call"], 3), "unit": "ms", "higher_is_better": False,
@@ -542,6 +650,7 @@ def main():
                       "value": round(r["tflops"], 1), "unit": "TFLOP/s",
                       "frac_of_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
                       "ms_per_step": round(r["ms_per_step"], 4), "per_linear": r["per_linear"]})
+        cpu_jobs.append((extra[-1], "chain", dict(r["host"], T=r["T"], flops=r["flops"])))
         print(f"[bench] C5 chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s",
               file=sys.stderr, flush=True)
         for fp8 in (False, True):
@@ -551,6 +660,7 @@ def main():
             extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N=14336 K=4096",
                           "value": round(r["tops"], 1), "unit": "TOPS",
                           "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4)})
+            cpu_jobs.append((extra[-1], "fp8" if fp8 else "i8", r["host"]))
         torch.cuda.synchronize()
         extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, 50, 30))
         r = bench_mxfp4(lib, timer, torch, 2048, 14336, 4096, 50, 30)
@@ -568,6 +678,11 @@ def main():
                 qz.cpu().numpy().view(np.uint32))
         xh = x.cpu().view(torch.int16).numpy().view(np.uint16)
         cpu = cpu_baseline(host, xh, N, K, group, args.cpu_seconds)
+        print(f"[bench] CPU baseline C2: {cpu['value']} GB/s", file=sys.stderr, flush=True)
+        sys.path.insert(0, os.path.join(REPO, "oracle"))
+        from py_oracle import Oracle
+        cpu_legs(Oracle(perf=True), cpu_jobs, min(3.0, args.cpu_seconds))
+        print(f"[bench] CPU legs done ({len(cpu_jobs)} configs)", file=sys.stderr, flush=True)
 
     # per-launch duration = back-to-back time / launches (>= kernel time; it
     # matches rocprofv3's kernel-trace average to within the launch gap)

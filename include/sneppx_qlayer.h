@@ -64,6 +64,14 @@ int SNEPPX_qlayer_save(const SNEPPXQLayer* layer, SNEPPXQStoreWriter* w, const c
 
 void SNEPPX_qlayer_destroy(SNEPPXQLayer* layer);
 
+/* Bias of the layer, fp32 [N] (the `bias` of QuantizedLinear,
+ * bindings/python/.../quantization.py:451-454): every forward then returns
+ * x . W + bias.  From host memory (synchronous) or device memory; NULL
+ * removes it.  SNEPPX_qlayer_save writes it as <prefix>.bias and
+ * SNEPPX_qlayer_load reads it back when present. */
+int SNEPPX_qlayer_set_bias(SNEPPXQLayer* layer, const float* bias, SNEPPXStream stream);
+int SNEPPX_qlayer_set_bias_device(SNEPPXQLayer* layer, const float* d_bias, SNEPPXStream stream);
+
 /* K, N and format of a layer. */
 size_t SNEPPX_qlayer_in_features(const SNEPPXQLayer* layer);
 size_t SNEPPX_qlayer_out_features(const SNEPPXQLayer* layer);
@@ -79,7 +87,10 @@ int SNEPPX_qlayer_forward_bf16(const SNEPPXQLayer* layer, const uint16_t* d_x, u
                                size_t M, SNEPPXStream stream);
 
 /* Host buffers in and out (the reference's tensors): copy x in, run, copy y
- * out, return when y is in host memory. */
+ * out, return when y is in host memory.  Reentrant like the matmul_3d it
+ * replaces: each call stages its buffers in device memory of its own, on a
+ * stream of its own, so host threads may call it at the same time (on one
+ * layer or several). */
 int SNEPPX_qlayer_matmul_host(const SNEPPXQLayer* layer, const float* x, float* y, size_t M);
 
 #ifdef __cplusplus

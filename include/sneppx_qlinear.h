@@ -20,6 +20,10 @@
  *          Groups are `group` contiguous columns, or given per column by
  *          g_idx int32 [K] (GPTQ act-order) with G groups.
  *   x/y    bf16 (uint16 bit patterns) or fp32 as stated per function.
+ *   bias   fp32 [N] or NULL: every linear computes y = x . W^T + bias, the
+ *          bias added to the fp32 result before the output is rounded (the
+ *          `out = out + self.bias` of QuantizedLinear.forward,
+ *          bindings/python/.../quantization.py:451-454).
  * Failure text: SNEPPX_qlinear_last_error() (thread-local, last failing call).
  */
 #ifndef SNEPPX_QLINEAR_H
@@ -90,9 +94,10 @@ int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* sc
 /* ---- quantized linears ---------------------------------------------------- */
 
 /* C1: W8 weight-only, fp32 activations: y[m][n] = s[n] * sum_k x[m][k]*q[n][k]
- * (fp32).  x fp32 [M][K], y fp32 [M][N].  Decode GEMV, HBM-bound. */
+ * (+ bias[n]) in fp32.  x fp32 [M][K], y fp32 [M][N].  Decode GEMV, HBM-bound. */
 int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* scales,
-                           float* y, size_t M, size_t N, size_t K, SNEPPXStream stream);
+                           const float* bias, float* y, size_t M, size_t N, size_t K,
+                           SNEPPXStream stream);
 
 /* C2/C3/C5: W4A16.  x bf16 [M][K]; y [M][N] in y_dtype (SNEPPX_BFLOAT16 or
  * SNEPPX_FLOAT32); fp32 accumulation.  qzeros NULL => symmetric zero 8.
@@ -100,8 +105,8 @@ int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* s
  * [0, G).  Small M runs the decode GEMV; large M the MFMA prefill GEMM. */
 int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
                          const uint32_t* qzeros, const int32_t* g_idx, size_t G,
-                         void* y, SNEPPXDtype y_dtype, size_t M, size_t N, size_t K,
-                         int group, SNEPPXStream stream);
+                         const float* bias, void* y, SNEPPXDtype y_dtype, size_t M, size_t N,
+                         size_t K, int group, SNEPPXStream stream);
 
 /* C3 fast path, step 1 (once per layer, at load time): GPTQ act-order
  * weights (qweight in column order k, g_idx int32 [K]) -> group-contiguous
@@ -120,8 +125,9 @@ int SNEPPX_qlinear_w4_actorder_prepare(const uint32_t* qweight, const int32_t* g
  * inside the decode kernel (M <= 4) or by one gather pass (other M). */
 int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sorted,
                                   const uint16_t* scales, const uint32_t* qzeros,
-                                  const uint16_t* perm, void* y, SNEPPXDtype y_dtype,
-                                  size_t M, size_t N, size_t K, int group, SNEPPXStream stream);
+                                  const uint16_t* perm, const float* bias, void* y,
+                                  SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
+                                  SNEPPXStream stream);
 
 /* C5 SwiGLU step between the gate/up and down projections (no reference
  * counterpart; the reference's MLP is fp32): gate_up bf16 [T][2F] with gate
@@ -144,12 +150,12 @@ int SNEPPX_qlinear_silu_mul_quant_int8(const uint16_t* gate_up, int8_t* q, float
 int SNEPPX_dev_quantize_int8_channel_bf16(const uint16_t* in, int8_t* q, float* scales,
                                           size_t rows, size_t cols, SNEPPXStream stream);
 
-/* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n]), acc = sum_k A*W in
- * int32 (exact).  A int8 [M][K] (per-token scales sA fp32 [M]), W int8 [N][K]
- * (per-channel sW fp32 [N]), out bf16 [M][N]. */
+/* C4 int8: out[m][n] = bf16(((float)acc * sA[m]) * sW[n] (+ bias[n])),
+ * acc = sum_k A*W in int32 (exact).  A int8 [M][K] (per-token scales sA fp32
+ * [M]), W int8 [N][K] (per-channel sW fp32 [N]), out bf16 [M][N]. */
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W,
-                           const float* sW, uint16_t* out, size_t M, size_t N, size_t K,
-                           SNEPPXStream stream);
+                           const float* sW, const float* bias, uint16_t* out, size_t M,
+                           size_t N, size_t K, SNEPPXStream stream);
 
 /* C4 int8 accumulators only: C int32 [M][N] = A . W^T (for bit-exact checks). */
 int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C,
@@ -157,10 +163,10 @@ int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C,
 
 /* C4 fp8: A, W are reference E4M3 codes (|x/s| < 256 so every code is an
  * OCP e4m3fn value of equal magnitude); per-tensor scales sA, sW are device
- * floats; fp32 accumulation; out bf16 [M][N] = bf16((acc * sA) * sW). */
+ * floats; fp32 accumulation; out bf16 [M][N] = bf16((acc * sA) * sW (+ bias[n])). */
 int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W,
-                            const float* sW, uint16_t* out, size_t M, size_t N, size_t K,
-                            SNEPPXStream stream);
+                            const float* sW, const float* bias, uint16_t* out, size_t M,
+                            size_t N, size_t K, SNEPPXStream stream);
 
 #ifdef __cplusplus
 }

@@ -11,16 +11,19 @@
  *
  * Library: libsneppx_quant.so (sneppx-alg_amd/).  A failed HIP call makes a
  * function return -1; SNEPPX_qlinear_last_error() then names the cause.
+ *
+ * Two guarded parts.  The types sit under the reference header's own guard
+ * (SNEPPX_QUANTIZATION_H): they are the reference's types, so a translation
+ * unit that already included the reference header keeps its definitions.
+ * The prototypes sit under their own guard, so in such a unit they
+ * redeclare the reference's 22 functions, and any difference in a return or
+ * argument type is a compile error (tests/test_abi.py builds exactly that).
  */
 #ifndef SNEPPX_QUANTIZATION_H
 #define SNEPPX_QUANTIZATION_H
 
 #include <stddef.h>
 #include <stdint.h>
-
-#ifdef __cplusplus
-extern "C" {
-#endif
 
 /* multidimensional_tensor_engine.h:27-41 (ordinal ABI) */
 #ifndef SNEPPX_DTYPE_DEFINED
@@ -77,6 +80,18 @@ typedef struct {
     size_t cols;
     int group_size;
 } SNEPPXGPTQState;
+
+#endif /* SNEPPX_QUANTIZATION_H: the reference's types */
+
+#ifndef SNEPPX_QUANTIZATION_API_H
+#define SNEPPX_QUANTIZATION_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
 
 /* replaces quantization.h:80-81 / quantize_int8.c:43-65 */
 int SNEPPX_quantize_int8_sym(const float* input, int8_t* output,
@@ -147,4 +162,4 @@ const char* SNEPPX_quant_mode_name(SNEPPXQuantMode mode);
 }
 #endif
 
-#endif /* SNEPPX_QUANTIZATION_H */
+#endif /* SNEPPX_QUANTIZATION_API_H */

@@ -132,6 +132,10 @@ int orc_w4a16_linear(const uint16_t* x_bf16, const uint32_t* qweight,
                      const int32_t* g_idx, size_t M, size_t N, size_t K,
                      int group, float* y);
 
+/* Bias term of QuantizedLinear.forward (quantization.py:451-454):
+ * y[m][n] = y[m][n] + bias[n], one fp32 add after the product. */
+void orc_add_bias(float* y, const float* bias, size_t M, size_t N);
+
 /* C1 / a19: y[m][n] = sum_k x[m][k] * ((float)q[n][k] * s[n]), k ascending */
 int orc_w8_linear(const float* x, const int8_t* q, const float* s,
                   size_t M, size_t N, size_t K, float* y);

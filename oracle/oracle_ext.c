@@ -256,6 +256,15 @@ int orc_w4a16_linear(const uint16_t* x_bf16, const uint32_t* qweight,
     return rc;
 }
 
+/* quantization.py:453-454: `out = out + self.bias` on the fp32 product
+ * (numpy broadcasts bias[n] over the rows). */
+void orc_add_bias(float* y, const float* bias, size_t M, size_t N)
+{
+    for (size_t m = 0; m < M; m++)
+        for (size_t n = 0; n < N; n++)
+            y[m * N + n] = y[m * N + n] + bias[n];
+}
+
 int orc_w8_linear(const float* x, const int8_t* q, const float* s,
                   size_t M, size_t N, size_t K, float* y)
 {

@@ -89,6 +89,7 @@ _ORACLE_ONLY = {
     "w8_linear": (C.c_int, [_f32p, _i8p, _f32p, _sz, _sz, _sz, _f32p]),
     "i8_gemm_i32": (None, [_i8p, _i8p, _i32p, _sz, _sz, _sz]),
     "w8a8_epilogue": (None, [_i32p, _f32p, _f32p, _sz, _sz, _f32p]),
+    "add_bias": (None, [_f32p, _f32p, _sz, _sz]),
     "quantize_fp8_e4m3_scaled": (C.c_int, [_f32p, _u8p, _sz, C.POINTER(C.c_float)]),
     "fp8_gemm": (None, [_u8p, _u8p, C.c_float, C.c_float, _sz, _sz, _sz, _f32p]),
 }
@@ -311,7 +312,17 @@ class Oracle(_Lib):
         rc = self.raw["w4_dequantize"](qweight, scales, _ptr(qz), _ptr(gi), N, K, group, out)
         return rc, out
 
-    def w4a16_linear(self, x_bf16, qweight, scales, qzeros, g_idx, N, K, group):
+    def add_bias(self, y, bias):
+        """y + bias[n] in fp32 (quantization.py:453-454), on a copy of y."""
+        y = np.array(y, np.float32, copy=True, order="C")
+        M, N = y.shape
+        self.raw["add_bias"](y, np.ascontiguousarray(bias, np.float32), M, N)
+        return y
+
+    def _bias(self, rc, y, bias):
+        return (rc, y) if bias is None or rc != 0 else (rc, self.add_bias(y, bias))
+
+    def w4a16_linear(self, x_bf16, qweight, scales, qzeros, g_idx, N, K, group, bias=None):
         x_bf16 = np.ascontiguousarray(x_bf16, np.uint16)
         M = x_bf16.shape[0]
         qweight = np.ascontiguousarray(qweight, np.uint32)
@@ -320,9 +331,9 @@ class Oracle(_Lib):
         gi = None if g_idx is None else np.ascontiguousarray(g_idx, np.int32)
         y = np.zeros((M, N), np.float32)
         rc = self.raw["w4a16_linear"](x_bf16, qweight, scales, _ptr(qz), _ptr(gi), M, N, K, group, y)
-        return rc, y
+        return self._bias(rc, y, bias)
 
-    def w8_linear(self, x, q, s):
+    def w8_linear(self, x, q, s, bias=None):
         x = np.ascontiguousarray(x, np.float32)
         q = np.ascontiguousarray(q, np.int8)
         s = np.ascontiguousarray(s, np.float32)
@@ -330,7 +341,7 @@ class Oracle(_Lib):
         N = q.shape[0]
         y = np.zeros((M, N), np.float32)
         rc = self.raw["w8_linear"](x, q, s, M, N, K, y)
-        return rc, y
+        return self._bias(rc, y, bias)
 
     def i8_gemm_i32(self, A, W):
         A = np.ascontiguousarray(A, np.int8)
@@ -341,13 +352,13 @@ class Oracle(_Lib):
         self.raw["i8_gemm_i32"](A, W, Cm, M, N, K)
         return Cm
 
-    def w8a8_epilogue(self, acc, sA, sW):
+    def w8a8_epilogue(self, acc, sA, sW, bias=None):
         acc = np.ascontiguousarray(acc, np.int32)
         M, N = acc.shape
         out = np.zeros((M, N), np.float32)
         self.raw["w8a8_epilogue"](acc, np.ascontiguousarray(sA, np.float32),
                                   np.ascontiguousarray(sW, np.float32), M, N, out)
-        return out
+        return out if bias is None else self.add_bias(out, bias)
 
     def quantize_fp8_e4m3_scaled(self, x):
         x = np.ascontiguousarray(x, np.float32)
@@ -356,14 +367,14 @@ class Oracle(_Lib):
         rc = self.raw["quantize_fp8_e4m3_scaled"](x, c, x.size, C.byref(s))
         return rc, c, np.float32(s.value)
 
-    def fp8_gemm(self, A, W, sA, sW):
+    def fp8_gemm(self, A, W, sA, sW, bias=None):
         A = np.ascontiguousarray(A, np.uint8)
         W = np.ascontiguousarray(W, np.uint8)
         M, K = A.shape
         N = W.shape[0]
         out = np.zeros((M, N), np.float32)
         self.raw["fp8_gemm"](A, W, sA, sW, M, N, K, out)
-        return out
+        return out if bias is None else self.add_bias(out, bias)
 
 
 class _WeightTensor(C.Structure):

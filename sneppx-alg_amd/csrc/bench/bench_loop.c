@@ -18,8 +18,8 @@ int snxb_loop_w4a16(int steps, int copies, const uint16_t* x, const uint32_t* co
                     size_t M, size_t N, size_t K, int group, SNEPPXStream stream) {
     for (int i = 0; i < steps; i++) {
         const int c = i % copies;
-        if (SNEPPX_qlinear_w4a16(x, qw[c], sc[c], qz ? qz[c] : NULL, NULL, 0, y, (SNEPPXDtype)y_dtype,
-                                 M, N, K, group, stream))
+        if (SNEPPX_qlinear_w4a16(x, qw[c], sc[c], qz ? qz[c] : NULL, NULL, 0, NULL, y,
+                                 (SNEPPXDtype)y_dtype, M, N, K, group, stream))
             return -1;
     }
     return 0;
@@ -30,8 +30,8 @@ int snxb_loop_w4a16_actorder(int steps, int copies, const uint16_t* x, const uin
                              size_t M, size_t N, size_t K, int group, SNEPPXStream stream) {
     for (int i = 0; i < steps; i++) {
         const int c = i % copies;
-        if (SNEPPX_qlinear_w4a16_actorder(x, qw[c], sc[c], NULL, perm, y, (SNEPPXDtype)y_dtype, M, N,
-                                          K, group, stream))
+        if (SNEPPX_qlinear_w4a16_actorder(x, qw[c], sc[c], NULL, perm, NULL, y, (SNEPPXDtype)y_dtype,
+                                          M, N, K, group, stream))
             return -1;
     }
     return 0;
@@ -42,7 +42,7 @@ int snxb_loop_w8_gemv(int steps, int copies, const float* x, const int8_t* const
                       SNEPPXStream stream) {
     for (int i = 0; i < steps; i++) {
         const int c = i % copies;
-        if (SNEPPX_qlinear_w8_gemv(x, q[c], s[c], y, M, N, K, stream)) return -1;
+        if (SNEPPX_qlinear_w8_gemv(x, q[c], s[c], NULL, y, M, N, K, stream)) return -1;
     }
     return 0;
 }

@@ -55,7 +55,9 @@ __global__ void __launch_bounds__(256) k_i8_gemm(const int8_t* __restrict__ A,
                                                  const float* __restrict__ sA,
                                                  const float* __restrict__ sW,
                                                  int32_t* __restrict__ Craw,
-                                                 uint16_t* __restrict__ out, int M, int N, int K) {
+                                                 uint16_t* __restrict__ out,
+                                                 const float* __restrict__ bias, int M, int N,
+                                                 int K) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.y * 64 + (wave >> 1) * 32, n0 = blockIdx.x * 64 + (wave & 1) * 32;
     const int r16 = lane & 15, kq = lane >> 4;
@@ -89,7 +91,8 @@ __global__ void __launch_bounds__(256) k_i8_gemm(const int8_t* __restrict__ A,
                 if (RAW)
                     Craw[(size_t)m * N + n] = acc[i][j][e];
                 else
-                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sA[m] * sW[n]);
+                    out[(size_t)m * N + n] = f32_to_bf16((float)acc[i][j][e] * sA[m] * sW[n] +
+                                                         (bias ? bias[n] : 0.0f));
             }
         }
 }
@@ -103,7 +106,9 @@ __global__ void __launch_bounds__(256) k_fp8_gemm(const uint8_t* __restrict__ A,
                                                   const uint8_t* __restrict__ W,
                                                   const float* __restrict__ sA,
                                                   const float* __restrict__ sW,
-                                                  uint16_t* __restrict__ out, int M, int N, int K) {
+                                                  uint16_t* __restrict__ out,
+                                                  const float* __restrict__ bias, int M, int N,
+                                                  int K) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int m0 = blockIdx.y * 64 + (wave >> 1) * 32, n0 = blockIdx.x * 64 + (wave & 1) * 32;
     const int r16 = lane & 15, kq = lane >> 4;
@@ -132,10 +137,11 @@ __global__ void __launch_bounds__(256) k_fp8_gemm(const uint8_t* __restrict__ A,
         for (int j = 0; j < 2; j++) {
             const int n = n0 + j * 16 + r16;
             if (n >= N) continue;
+            const float bv = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 const int m = m0 + i * 16 + kq * 4 + e;
-                if (m < M) out[(size_t)m * N + n] = f32_to_bf16(acc[i][j][e] * sa * sw);
+                if (m < M) out[(size_t)m * N + n] = f32_to_bf16(acc[i][j][e] * sa * sw + bv);
             }
         }
 }
@@ -167,8 +173,9 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                                                  const float* __restrict__ sA,
                                                  const float* __restrict__ sW,
                                                  int32_t* __restrict__ Craw,
-                                                 uint16_t* __restrict__ out, int M, int N, int K,
-                                                 int tiles_m, int tiles_n) {
+                                                 uint16_t* __restrict__ out,
+                                                 const float* __restrict__ bias, int M, int N,
+                                                 int K, int tiles_m, int tiles_n) {
     constexpr int FM = 4;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -218,7 +225,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
 
     dload(0, 0);
     // epilogue scales, fetched now so their latency hides under the K loop
-    float sa[FM][4], swv[TFN];
+    float sa[FM][4], swv[TFN], bv[TFN];
     if (!RAW) {
 #pragma unroll
         for (int i = 0; i < FM; i++)
@@ -231,6 +238,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
         for (int j = 0; j < TFN; j++) {
             const int n = n0 + wn * 112 + j * 16 + r16;
             swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
+            bv[j] = bias ? bias[n < N ? n : N - 1] : 0.0f;
         }
     }
     for (int kt = 0; kt < nk; kt++) {
@@ -294,7 +302,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                 if (RAW)
                     Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
                 else
-                    out[(size_t)m * N + n] = bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j]);
+                    out[(size_t)m * N + n] = bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j] + bv[j]);
             }
         }
     }
@@ -476,7 +484,8 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
                                                     const float* __restrict__ sA,
                                                     const float* __restrict__ sW,
                                                     int32_t* __restrict__ Craw,
-                                                    uint16_t* __restrict__ out, int M, int N,
+                                                    uint16_t* __restrict__ out,
+                                                    const float* __restrict__ bias, int M, int N,
                                                     int K, int tiles_m, int tiles_n) {
     constexpr int FN = TBN / 32;                 // 7 blocks per wave
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
@@ -521,7 +530,7 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
     const int nk = K / TBK;
 
     dload(0, 0);
-    float sa[16], swv[FN];
+    float sa[16], swv[FN], bv[FN];
     if (!RAW) {
 #pragma unroll
         for (int v = 0; v < 16; v++) {
@@ -532,6 +541,7 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
         for (int j = 0; j < FN; j++) {
             const int n = n0 + j * 32 + r32;
             swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
+            bv[j] = bias ? bias[n < N ? n : N - 1] : 0.0f;
         }
     }
     for (int kt = 0; kt < nk; kt++) {
@@ -598,7 +608,7 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
 #pragma unroll
         for (int v = 0; v < 16; v++)
             ct[(8 * (v >> 2) + 4 * h + (v & 3)) * XCROW + j * 32 + r32] =
-                bf16_out((float)acc[j][v] * sa[v] * swv[j]);
+                bf16_out((float)acc[j][v] * sa[v] * swv[j] + bv[j]);
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 #pragma unroll
     for (int t = 0; t < 14; t++) {        // 32 rows x 28 pieces = 896 = 14 x 64
@@ -634,14 +644,15 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
 // would also wait for the next stage's loads and the previous tile's stores.
 constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every output buffer
 
-template <bool RAW>
+template <bool RAW, bool BIAS>
 __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
                                                   const int8_t* __restrict__ W,
                                                   const float* __restrict__ sA,
                                                   const float* __restrict__ sW,
                                                   int32_t* __restrict__ Craw,
-                                                  uint16_t* __restrict__ out, int M, int N, int K,
-                                                  int tiles_m, int tiles_n) {
+                                                  uint16_t* __restrict__ out,
+                                                  const float* __restrict__ bias, int M, int N,
+                                                  int K, int tiles_m, int tiles_n) {
     constexpr int FN = TBN / 32;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -781,6 +792,14 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
             }
         } else {
             uint16_t* ct = reinterpret_cast<uint16_t*>(lds + (buf ^ 1) * TLDS_STAGE) + wave * (16 * XCROW);
+            // the bias is read here rather than before the K loop (the loop
+            // already holds every register), and only in the BIAS build
+            float bv[FN];
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = n0 + j * 32 + r32;
+                bv[j] = BIAS ? bias[n < N ? n : N - 1] : 0.0f;
+            }
 #pragma unroll
             for (int p = 0; p < 2; p++) {         // rows 16 p .. 16 p + 15 of the wave's 32
 #pragma unroll
@@ -788,7 +807,8 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
 #pragma unroll
                     for (int v = 8 * p; v < 8 * p + 8; v++)
                         ct[(8 * (v >> 2) + 4 * h + (v & 3) - 16 * p) * XCROW + j * 32 + r32] =
-                            bf16_out((float)acc[j][v] * sa[v] * swv[j]);
+                            BIAS ? bf16_out((float)acc[j][v] * sa[v] * swv[j] + bv[j])
+                                 : bf16_out((float)acc[j][v] * sa[v] * swv[j]);
 #pragma unroll
                 for (int q = 0; q < 7; q++) {     // 16 rows x 28 pieces of 16 B = 7 x 64
                     const int qd = q * 64 + lane;
@@ -809,9 +829,9 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
     __builtin_amdgcn_s_waitcnt(0x0070);       // the spare stage-0 loads land before exit
 }
 
-template <bool RAW>
+template <bool RAW, bool BIAS>
 int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
-               uint16_t* out, int M, int N, int K, hipStream_t st) {
+               uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const int ntiles = tiles_m * tiles_n;
     const int ncu = snx::cu_count();
@@ -820,18 +840,19 @@ int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* s
     if (grid > ntiles) grid = ntiles;
     const size_t lds = 2 * (size_t)TLDS_STAGE;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_gemm_i8p<RAW>);
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_i8p<RAW, BIAS>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_i8p<RAW><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K, tiles_m, tiles_n);
+    k_gemm_i8p<RAW, BIAS><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m,
+                                                  tiles_n);
     return snx_launch_check("k_gemm_i8p");
 }
 
 template <bool FP8, bool RAW>
 int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
-                 int32_t* Craw, uint16_t* out, int M, int N, int K, hipStream_t st) {
+                 int32_t* Craw, uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     if ((uint64_t)M * K >= (1ull << 32) || (uint64_t)N * K >= (1ull << 32)) {
         snx_set_error("gemm: operands above 4 GiB are not supported");
@@ -844,14 +865,14 @@ int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* s
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_x32<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
-                                                          tiles_m, tiles_n);
+    k_gemm_x32<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
+                                                              K, tiles_m, tiles_n);
     return snx_launch_check("k_gemm_x32");
 }
 
 template <bool FP8, bool RAW>
 int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
-                 uint16_t* out, int M, int N, int K, hipStream_t st) {
+                 uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     if ((uint64_t)M * K >= (1ull << 32) || (uint64_t)N * K >= (1ull << 32)) {
         snx_set_error("gemm: operands above 4 GiB are not supported");
@@ -864,8 +885,8 @@ int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float*
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_8w<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, M, N, K,
-                                                            tiles_m, tiles_n);
+    k_gemm_8w<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
+                                                            K, tiles_m, tiles_n);
     return snx_launch_check("k_gemm_8w");
 }
 
@@ -874,7 +895,8 @@ int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float*
 extern "C" {
 
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
-                  int32_t* c_i32, uint16_t* out_bf16, size_t M, size_t N, size_t K, void* st) {
+                  int32_t* c_i32, uint16_t* out_bf16, const float* bias, size_t M, size_t N,
+                  size_t K, void* st) {
     if (K % 16 != 0) {
         snx_set_error("i8 gemm: K=%zu must be a multiple of 16", K);
         return -1;
@@ -884,17 +906,18 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
         // and writes bf16 output in 16-byte row pieces
         const bool fits = (uint64_t)M * K < (1ull << 31) && (uint64_t)N * K < (1ull << 31);
         if (c_i32)
-            return fits ? launch_i8p<true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st))
-                        : launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+            return fits ? launch_i8p<true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+                        : launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
         if (fits && N % 8 == 0 && (reinterpret_cast<uintptr_t>(out_bf16) & 15) == 0 && (uint64_t)M * N * 2 < BUF_DROP)
-            return launch_i8p<false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
-        return launch_x32<false, false>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K, S(st));
+            return bias ? launch_i8p<false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+                        : launch_i8p<false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
+        return launch_x32<false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
     }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     if (c_i32)
-        k_i8_gemm<true><<<grid, 256, 0, S(st)>>>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K);
+        k_i8_gemm<true><<<grid, 256, 0, S(st)>>>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K);
     else
-        k_i8_gemm<false><<<grid, 256, 0, S(st)>>>(A, W, sA, sW, c_i32, out_bf16, (int)M, (int)N, (int)K);
+        k_i8_gemm<false><<<grid, 256, 0, S(st)>>>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K);
     return snx_launch_check("k_i8_gemm");
 }
 
@@ -909,16 +932,16 @@ int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W,
 }
 
 int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const float* sW,
-                   uint16_t* out_bf16, size_t M, size_t N, size_t K, void* st) {
+                   uint16_t* out_bf16, const float* bias, size_t M, size_t N, size_t K, void* st) {
     if (K % 32 != 0) {
         snx_set_error("fp8 gemm: K=%zu must be a multiple of 32", K);
         return -1;
     }
     if (K % TBK == 0 && M >= 128 && N >= 128)
         return launch_tiled<true, false>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(W),
-                                         sA, sW, nullptr, out_bf16, (int)M, (int)N, (int)K, S(st));
+                                         sA, sW, nullptr, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
-    k_fp8_gemm<<<grid, 256, 0, S(st)>>>(A, W, sA, sW, out_bf16, (int)M, (int)N, (int)K);
+    k_fp8_gemm<<<grid, 256, 0, S(st)>>>(A, W, sA, sW, out_bf16, bias, (int)M, (int)N, (int)K);
     return snx_launch_check("k_fp8_gemm");
 }
 

@@ -50,7 +50,9 @@ template <int R>
 __global__ void __launch_bounds__(256) k_w8_gemv(const float* __restrict__ x,
                                                  const int8_t* __restrict__ q,
                                                  const float* __restrict__ s,
-                                                 float* __restrict__ y, int M, int N, int K) {
+                                                 float* __restrict__ y,
+                                                 const float* __restrict__ bias, int M, int N,
+                                                 int K) {
     const int lane = threadIdx.x & 63;
     const int n0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * R;
     if (n0 >= N) return;
@@ -80,7 +82,11 @@ __global__ void __launch_bounds__(256) k_w8_gemv(const float* __restrict__ x,
 #pragma unroll
         for (int r = 0; r < R; r++) {
             float v = wave_sum(acc[r]);
-            if (lane == 0 && n0 + r < N) y[(size_t)m * N + n0 + r] = s[n0 + r] * v;
+            if (lane == 0 && n0 + r < N) {
+                float o = s[n0 + r] * v;
+                if (bias) o += bias[n0 + r];
+                y[(size_t)m * N + n0 + r] = o;
+            }
         }
     }
 }
@@ -103,23 +109,24 @@ __device__ __forceinline__ float dpp_sum_to_lane63(float v) {
 }
 
 // M = 1, K = 1024 SL: a workgroup of 16 waves (one output row each) stages
-// x (fp32) once in LDS and sums it; lane l of a wave loads bytes
-// [16 l, +16) of every 1 KB slice of its row (nontemporal 16-byte loads, all
-// SL in flight before the first FMA).  Bytes are read as unsigned
-// (b ^ 0x80 = b + 128) with v_cvt_f32_ubyte*, and 128 * sum(x) comes off
-// the wave total: sum x*b = sum x*(b + 128) - 128 * sum x.  The lane's 16
-// activations of a slice sit at (slice * 64 + lane) * 80 bytes, so the
-// 16-byte LDS reads of a wave are free of bank conflicts.  Summing x once
-// per workgroup instead of per lane removes a 16*SL-long dependent add chain
-// from every wave.
+// x (fp32) once in LDS; lane l of a wave loads bytes [16 l, +16) of every
+// 1 KB slice of its row (nontemporal 16-byte loads, all SL in flight before
+// the first FMA).  Bytes are read as unsigned (b ^ 0x80 = b + 128) with
+// v_cvt_f32_ubyte*, and 128 * sum(x) comes off per 16-column slot:
+// sum x*b = sum over slots of (sum x*(b + 128) - 128 * sum x), so the
+// partial sums stay the size of the result even for activations far from
+// zero mean.  The lane's 16 activations of a slot sit at
+// (slice * 64 + lane) * 80 bytes, so the 16-byte LDS reads of a wave are free
+// of bank conflicts; the slot's sum of x, computed once per workgroup at
+// staging, sits in the 16 bytes of padding after them.
 template <int SL>
 __global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
                                                    const int8_t* __restrict__ q,
                                                    const float* __restrict__ s,
-                                                   float* __restrict__ y, int N) {
+                                                   float* __restrict__ y,
+                                                   const float* __restrict__ bias, int N) {
     constexpr int K = 1024 * SL, NIT = K / 4, NTHR = 1024, XPT = (NIT + NTHR - 1) / NTHR;
-    extern __shared__ __attribute__((aligned(16))) float xl[];   // [SL * 64][20], then [16]
-    float* wsum = xl + SL * 64 * 20;
+    extern __shared__ __attribute__((aligned(16))) float xl[];   // [SL * 64][16 x + sum + pad]
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int n0 = blockIdx.x * 16 + wave;
@@ -143,18 +150,19 @@ __global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
         w[sl] = __builtin_nontemporal_load(
             reinterpret_cast<const u32x4*>(q + (size_t)n * K + sl * 1024 + lane * 16));
     asm volatile("" ::: "memory");
-    float part = 0.0f;
+    // item it holds columns 4 it .. 4 it + 3 of slot it / 4; the four items
+    // of a slot sit in four consecutive lanes (NTHR % 4 == 0)
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         const int it = tid + i * NTHR;
+        float part = (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w);
+        part += dpp_mv<0xB1, 0xF>(part);   // quad_perm [1,0,3,2]
+        part += dpp_mv<0x4E, 0xF>(part);   // quad_perm [2,3,0,1]
         if (it < NIT) {
-            const int col = it * 4, sl = col >> 10, l = (col & 1023) >> 4, qq = (col & 15) >> 2;
-            reinterpret_cast<float4*>(xl)[(sl * 64 + l) * 5 + qq] = xr[i];
-            part += (xr[i].x + xr[i].y) + (xr[i].z + xr[i].w);
+            reinterpret_cast<float4*>(xl)[(it >> 2) * 5 + (it & 3)] = xr[i];
+            if ((it & 3) == 0) xl[(it >> 2) * 20 + 16] = part;
         }
     }
-    part = dpp_sum_to_lane63(part);
-    if (lane == 63) wsum[wave] = part;
     __syncthreads();
 
     float acc = 0.0f;
@@ -166,22 +174,23 @@ __global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
             const float4 v = reinterpret_cast<const float4*>(xl)[(sl * 64 + lane) * 5 + t];
             xv[4 * t] = v.x; xv[4 * t + 1] = v.y; xv[4 * t + 2] = v.z; xv[4 * t + 3] = v.w;
         }
+        float a = -128.0f * xl[(sl * 64 + lane) * 20 + 16];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const uint32_t u = w[sl][e] ^ 0x80808080u;
             // (float)(byte j of u) compiles to one v_cvt_f32_ubyte<j>
-            acc += xv[4 * e] * (float)(u & 0xFFu);
-            acc += xv[4 * e + 1] * (float)((u >> 8) & 0xFFu);
-            acc += xv[4 * e + 2] * (float)((u >> 16) & 0xFFu);
-            acc += xv[4 * e + 3] * (float)(u >> 24);
+            a += xv[4 * e] * (float)(u & 0xFFu);
+            a += xv[4 * e + 1] * (float)((u >> 8) & 0xFFu);
+            a += xv[4 * e + 2] * (float)((u >> 16) & 0xFFu);
+            a += xv[4 * e + 3] * (float)(u >> 24);
         }
+        acc += a;
     }
     acc = dpp_sum_to_lane63(acc);
     if (lane == 63 && n0 < N) {
-        float xt = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; i++) xt += wsum[i];
-        y[n0] = s[n0] * (acc - 128.0f * xt);
+        float o = s[n0] * acc;
+        if (bias) o += bias[n0];
+        y[n0] = o;
     }
 }
 
@@ -189,7 +198,9 @@ __global__ void __launch_bounds__(1024) k_w8_gemv1(const float* __restrict__ x,
 __global__ void __launch_bounds__(256) k_w8_gemv_any(const float* __restrict__ x,
                                                      const int8_t* __restrict__ q,
                                                      const float* __restrict__ s,
-                                                     float* __restrict__ y, int M, int N, int K) {
+                                                     float* __restrict__ y,
+                                                     const float* __restrict__ bias, int M, int N,
+                                                     int K) {
     const int lane = threadIdx.x & 63;
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
@@ -197,7 +208,7 @@ __global__ void __launch_bounds__(256) k_w8_gemv_any(const float* __restrict__ x
         float acc = 0.0f;
         for (int k = lane; k < K; k += 64) acc += x[(size_t)m * K + k] * (float)q[(size_t)n * K + k];
         acc = wave_sum(acc);
-        if (lane == 0) y[(size_t)m * N + n] = s[n] * acc;
+        if (lane == 0) y[(size_t)m * N + n] = bias ? s[n] * acc + bias[n] : s[n] * acc;
     }
 }
 
@@ -213,8 +224,9 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__
                                                     const uint32_t* __restrict__ qw,
                                                     const uint16_t* __restrict__ scales,
                                                     const uint32_t* __restrict__ qz,
-                                                    void* __restrict__ y, int M, int N, int K,
-                                                    int G, int group) {
+                                                    void* __restrict__ y,
+                                                    const float* __restrict__ bias, int M, int N,
+                                                    int K, int G, int group) {
     constexpr int CH = 8;                       // steps whose loads are in flight together
     __shared__ f32x4 red[4][MT][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -286,6 +298,7 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__
     for (int t = 0; t < MT; t++) {
         f32x4 v = red[0][t][lane] + red[1][t][lane] + red[2][t][lane] + red[3][t][lane];
         if (n0 + nl >= N) continue;
+        if (bias) v += bias[n0 + nl];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int m = t * 16 + kq * 4 + i;   // MFMA C layout: row 4*(lane/16)+i, col lane%16
@@ -319,8 +332,9 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
                                                           const uint16_t* __restrict__ scales,
                                                           const uint32_t* __restrict__ qz,
                                                           const uint16_t* __restrict__ perm,
-                                                          void* __restrict__ y, int M, int N,
-                                                          int K, int G, int gshift) {
+                                                          void* __restrict__ y,
+                                                          const float* __restrict__ bias, int M,
+                                                          int N, int K, int G, int gshift) {
     constexpr int CH = 8;
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const int xrow = K * 2 + 16;                               // bytes per staged row (+pad)
@@ -499,7 +513,8 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     red[wave * 64 + lane] = yacc;
     __syncthreads();
     if (wave != 0 || kq != 0 || n0 + nl >= N) return;
-    const f32x4 v = red[lane] + red[64 + lane] + red[128 + lane] + red[192 + lane];
+    f32x4 v = red[lane] + red[64 + lane] + red[128 + lane] + red[192 + lane];
+    if (bias) v += bias[n0 + nl];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         if (i >= M) break;
@@ -532,7 +547,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ scales,
                                                      const uint32_t* __restrict__ qz,
                                                      const uint16_t* __restrict__ perm,
-                                                     void* __restrict__ y, int N) {
+                                                     void* __restrict__ y,
+                                                     const float* __restrict__ bias, int N) {
     constexpr int K = 2048 * T, G = 16 * T, KW = K / 8, NCH = K / 32, NIT = K / 8;
     constexpr int RW = 2, WROWS = 16, NTHR = 512;
     constexpr int XPT = (NIT + NTHR - 1) / NTHR;
@@ -712,6 +728,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             if (n0 + r >= N) break;
+            if (bias) out[r] += bias[n0 + r];
             if (YF32)
                 reinterpret_cast<float*>(y)[n0 + r] = out[r];
             else
@@ -849,11 +866,13 @@ __global__ void __launch_bounds__(256) k_w4a16_splitk(const uint16_t* __restrict
 // y[m][n] = sum over s of part[s][m][n], s ascending
 __global__ void __launch_bounds__(256) k_w4a16_reduce(const float* __restrict__ part,
                                                       void* __restrict__ y, int y_f32, int S,
-                                                      size_t MN) {
+                                                      size_t MN, int N,
+                                                      const float* __restrict__ bias) {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= MN) return;
     float v = 0.0f;
     for (int s = 0; s < S; s++) v += part[(size_t)s * MN + i];
+    if (bias) v += bias[i % (size_t)N];
     if (y_f32)
         reinterpret_cast<float*>(y)[i] = v;
     else
@@ -867,6 +886,7 @@ struct W4Launch {
     const uint32_t* qz;
     const uint16_t* perm;
     void* y;
+    const float* bias;
     int y_f32, M, N, K, G, group;
     size_t lds;
     hipStream_t s;
@@ -878,7 +898,7 @@ int launch_small_vs(const W4Launch& a) {
     const int gshift = __builtin_ctz((unsigned)a.group);
 #define SNX_SMALL(Z, F)                                                                         \
     k_w4a16_gemv_small<XPT, MM, Z, F, VS, PERM><<<grid, block, a.lds, a.s>>>(                   \
-        a.x, a.qw, a.scales, a.qz, a.perm, a.y, a.M, a.N, a.K, a.G, gshift)
+        a.x, a.qw, a.scales, a.qz, a.perm, a.y, a.bias, a.M, a.N, a.K, a.G, gshift)
     if (a.qz) {
         if (a.y_f32) SNX_SMALL(true, true);
         else SNX_SMALL(true, false);
@@ -922,7 +942,7 @@ int launch_gemv1_t(const W4Launch& a) {
     }
 #define SNX_G1(Z, F)                                                                      \
     k_w4a16_gemv1<T, Z, F, PERM><<<grid, block, lds, a.s>>>(a.x, a.qw, a.scales, a.qz, a.perm, \
-                                                            a.y, a.N)
+                                                            a.y, a.bias, a.N)
     if (a.qz) {
         if (a.y_f32) SNX_G1(true, true);
         else SNX_G1(true, false);
@@ -988,7 +1008,9 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
                                                        const uint16_t* __restrict__ scales,
                                                        const uint32_t* __restrict__ qz,
                                                        const uint16_t* __restrict__ perm,
-                                                       void* __restrict__ y, int M, int N) {
+                                                       void* __restrict__ y,
+                                                       const float* __restrict__ bias, int M,
+                                                       int N) {
     constexpr int K = 1024 * NC, KW = K / 8, G = K / 128, ZW = (G + 7) / 8;
     constexpr int RS = K * 2 + 16;            // LDS row stride in bytes (16 B pad: no bank conflicts)
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1162,6 +1184,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
             for (int w = 0; w < 8; w++) v += red[(rb * 8 + w) * 64 + l][i];
             const int m = 4 * (l >> 4) + i, n = g * 16 + (l & 15);
             if (m < M && n < N) {
+                if (bias) v += bias[n];
                 if (YF32)
                     reinterpret_cast<float*>(y)[(size_t)m * N + n] = v;
                 else
@@ -1184,7 +1207,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
 
 template <int NC, bool Z, bool F, bool PERM>
 int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
-                   const uint16_t* perm, void* y, int M, int N, size_t lds, int grid, hipStream_t st) {
+                   const uint16_t* perm, void* y, const float* bias, int M, int N, size_t lds, int grid,
+                   hipStream_t st) {
     // the LDS size depends on M: opt in to the most any call may ask for
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
     const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>);
@@ -1192,31 +1216,31 @@ int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales
         snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_w4a16_gemv_mt<NC, Z, F, PERM><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, M, N);
+    k_w4a16_gemv_mt<NC, Z, F, PERM><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, bias, M, N);
     return snx_launch_check("k_w4a16_gemv_mt");
 }
 
 template <int NC, bool PERM>
 int launch_gemv_mt_nc(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
-                      const uint16_t* perm, void* y, int y_f32, int M, int N, size_t lds, int grid,
-                      hipStream_t st) {
+                      const uint16_t* perm, void* y, const float* bias, int y_f32, int M, int N,
+                      size_t lds, int grid, hipStream_t st) {
     if (qz) {
-        if (y_f32) return launch_gemv_mt<NC, true, true, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
-        return launch_gemv_mt<NC, true, false, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+        if (y_f32) return launch_gemv_mt<NC, true, true, PERM>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
+        return launch_gemv_mt<NC, true, false, PERM>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
     }
-    if (y_f32) return launch_gemv_mt<NC, false, true, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
-    return launch_gemv_mt<NC, false, false, PERM>(x, qw, scales, qz, perm, y, M, N, lds, grid, st);
+    if (y_f32) return launch_gemv_mt<NC, false, true, PERM>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
+    return launch_gemv_mt<NC, false, false, PERM>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
 }
 
 template <bool PERM>
 int launch_gemv_mt_k(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
-                     const uint16_t* perm, void* y, int y_f32, int M, int N, int K, size_t lds, int grid,
-                     hipStream_t st) {
+                     const uint16_t* perm, void* y, const float* bias, int y_f32, int M, int N, int K,
+                     size_t lds, int grid, hipStream_t st) {
     switch (K / 1024) {
-        case 1: return launch_gemv_mt_nc<1, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
-        case 2: return launch_gemv_mt_nc<2, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
-        case 3: return launch_gemv_mt_nc<3, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
-        default: return launch_gemv_mt_nc<4, PERM>(x, qw, scales, qz, perm, y, y_f32, M, N, lds, grid, st);
+        case 1: return launch_gemv_mt_nc<1, PERM>(x, qw, scales, qz, perm, y, bias, y_f32, M, N, lds, grid, st);
+        case 2: return launch_gemv_mt_nc<2, PERM>(x, qw, scales, qz, perm, y, bias, y_f32, M, N, lds, grid, st);
+        case 3: return launch_gemv_mt_nc<3, PERM>(x, qw, scales, qz, perm, y, bias, y_f32, M, N, lds, grid, st);
+        default: return launch_gemv_mt_nc<4, PERM>(x, qw, scales, qz, perm, y, bias, y_f32, M, N, lds, grid, st);
     }
 }
 
@@ -1226,8 +1250,9 @@ __global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restric
                                                        const uint16_t* __restrict__ scales,
                                                        const uint32_t* __restrict__ qz,
                                                        const int32_t* __restrict__ g_idx,
-                                                       void* __restrict__ y, int y_f32, int M,
-                                                       int N, int K, int G, int group) {
+                                                       void* __restrict__ y,
+                                                       const float* __restrict__ bias, int y_f32,
+                                                       int M, int N, int K, int G, int group) {
     const int lane = threadIdx.x & 63;
     const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (n >= N) return;
@@ -1249,6 +1274,7 @@ __global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restric
         }
         acc = wave_sum(acc);
         if (lane == 0) {
+            if (bias) acc += bias[n];
             if (y_f32)
                 reinterpret_cast<float*>(y)[(size_t)m * N + n] = acc;
             else
@@ -1259,16 +1285,19 @@ __global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restric
 
 template <int MT>
 int launch_w4a16(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                 const uint32_t* qz, void* y, int y_f32, int M, int N, int K, int G, int group,
-                 hipStream_t st) {
+                 const uint32_t* qz, void* y, const float* bias, int y_f32, int M, int N, int K,
+                 int G, int group, hipStream_t st) {
     dim3 grid((N + 15) / 16), block(256);
+#define SNX_W4(Z, F) \
+    k_w4a16_gemv<MT, Z, F><<<grid, block, 0, st>>>(x, qw, scales, qz, y, bias, M, N, K, G, group)
     if (qz) {
-        if (y_f32) k_w4a16_gemv<MT, true, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
-        else k_w4a16_gemv<MT, true, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        if (y_f32) SNX_W4(true, true);
+        else SNX_W4(true, false);
     } else {
-        if (y_f32) k_w4a16_gemv<MT, false, true><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
-        else k_w4a16_gemv<MT, false, false><<<grid, block, 0, st>>>(x, qw, scales, qz, y, M, N, K, G, group);
+        if (y_f32) SNX_W4(false, true);
+        else SNX_W4(false, false);
     }
+#undef SNX_W4
     return snx_launch_check("k_w4a16_gemv");
 }
 
@@ -1309,9 +1338,9 @@ __global__ void __launch_bounds__(256) k_w4_permute_cols(const uint32_t* __restr
 // k_w8_gemv1 at K = 1024 SL: the activations staged in LDS (SL * 5 KB; above
 // 64 KB from SL = 13 on, which needs the one-time opt-in)
 template <int SL>
-int launch_w8_gemv1(const float* x, const int8_t* q, const float* s, float* y, size_t N,
-                    hipStream_t st) {
-    const size_t lds = (size_t)SL * 64 * 20 * sizeof(float) + 16 * sizeof(float);
+int launch_w8_gemv1(const float* x, const int8_t* q, const float* s, float* y, const float* bias,
+                    size_t N, hipStream_t st) {
+    const size_t lds = (size_t)SL * 64 * 20 * sizeof(float);
     if (lds > 64 * 1024) {
         static std::atomic<uint64_t> lds_done{0};
         if (snx::lds_optin(reinterpret_cast<const void*>(&k_w8_gemv1<SL>), (int)lds, lds_done) != hipSuccess) {
@@ -1319,7 +1348,7 @@ int launch_w8_gemv1(const float* x, const int8_t* q, const float* s, float* y, s
             return -1;
         }
     }
-    k_w8_gemv1<SL><<<(unsigned)((N + 15) / 16), 1024, lds, st>>>(x, q, s, y, (int)N);
+    k_w8_gemv1<SL><<<(unsigned)((N + 15) / 16), 1024, lds, st>>>(x, q, s, y, bias, (int)N);
     return snx_launch_check("k_w8_gemv1");
 }
 
@@ -1352,8 +1381,10 @@ int snx_k_w4a16_splitk(const uint16_t* x, const uint32_t* qw, const uint16_t* sc
     return snx_launch_check("k_w4a16_splitk");
 }
 
-int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S_, size_t MN, void* st) {
-    k_w4a16_reduce<<<(unsigned)((MN + 255) / 256), 256, 0, S(st)>>>(part, y, y_f32, S_, MN);
+int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S_, size_t MN, size_t N,
+                       const float* bias, void* st) {
+    k_w4a16_reduce<<<(unsigned)((MN + 255) / 256), 256, 0, S(st)>>>(part, y, y_f32, S_, MN, (int)N,
+                                                                     bias);
     return snx_launch_check("k_w4a16_reduce");
 }
 
@@ -1371,34 +1402,36 @@ int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs
     return snx_launch_check("k_w4_permute_cols");
 }
 
-int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, size_t M, size_t N,
-                  size_t K, void* st) {
+int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, const float* bias,
+                  size_t M, size_t N, size_t K, void* st) {
     if (M == 1 && K % 1024 == 0 && K <= 16384) {
         switch (K / 1024) {
-            case 1: return launch_w8_gemv1<1>(x, q, s, y, N, S(st));
-            case 2: return launch_w8_gemv1<2>(x, q, s, y, N, S(st));
-            case 3: return launch_w8_gemv1<3>(x, q, s, y, N, S(st));
-            case 4: return launch_w8_gemv1<4>(x, q, s, y, N, S(st));
-            case 5: return launch_w8_gemv1<5>(x, q, s, y, N, S(st));
-            case 6: return launch_w8_gemv1<6>(x, q, s, y, N, S(st));
-            case 7: return launch_w8_gemv1<7>(x, q, s, y, N, S(st));
-            case 8: return launch_w8_gemv1<8>(x, q, s, y, N, S(st));
-            case 9: return launch_w8_gemv1<9>(x, q, s, y, N, S(st));
-            case 10: return launch_w8_gemv1<10>(x, q, s, y, N, S(st));
-            case 11: return launch_w8_gemv1<11>(x, q, s, y, N, S(st));
-            case 12: return launch_w8_gemv1<12>(x, q, s, y, N, S(st));
-            case 13: return launch_w8_gemv1<13>(x, q, s, y, N, S(st));
-            case 14: return launch_w8_gemv1<14>(x, q, s, y, N, S(st));
-            case 15: return launch_w8_gemv1<15>(x, q, s, y, N, S(st));
-            default: return launch_w8_gemv1<16>(x, q, s, y, N, S(st));
+            case 1: return launch_w8_gemv1<1>(x, q, s, y, bias, N, S(st));
+            case 2: return launch_w8_gemv1<2>(x, q, s, y, bias, N, S(st));
+            case 3: return launch_w8_gemv1<3>(x, q, s, y, bias, N, S(st));
+            case 4: return launch_w8_gemv1<4>(x, q, s, y, bias, N, S(st));
+            case 5: return launch_w8_gemv1<5>(x, q, s, y, bias, N, S(st));
+            case 6: return launch_w8_gemv1<6>(x, q, s, y, bias, N, S(st));
+            case 7: return launch_w8_gemv1<7>(x, q, s, y, bias, N, S(st));
+            case 8: return launch_w8_gemv1<8>(x, q, s, y, bias, N, S(st));
+            case 9: return launch_w8_gemv1<9>(x, q, s, y, bias, N, S(st));
+            case 10: return launch_w8_gemv1<10>(x, q, s, y, bias, N, S(st));
+            case 11: return launch_w8_gemv1<11>(x, q, s, y, bias, N, S(st));
+            case 12: return launch_w8_gemv1<12>(x, q, s, y, bias, N, S(st));
+            case 13: return launch_w8_gemv1<13>(x, q, s, y, bias, N, S(st));
+            case 14: return launch_w8_gemv1<14>(x, q, s, y, bias, N, S(st));
+            case 15: return launch_w8_gemv1<15>(x, q, s, y, bias, N, S(st));
+            default: return launch_w8_gemv1<16>(x, q, s, y, bias, N, S(st));
         }
     }
     if (K % 16 == 0) {
         constexpr int R = 4;
         size_t waves = (N + R - 1) / R;
-        k_w8_gemv<R><<<(unsigned)((waves + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, (int)M, (int)N, (int)K);
+        k_w8_gemv<R><<<(unsigned)((waves + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, bias, (int)M, (int)N,
+                                                                     (int)K);
     } else {
-        k_w8_gemv_any<<<(unsigned)((N + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, (int)M, (int)N, (int)K);
+        k_w8_gemv_any<<<(unsigned)((N + 3) / 4), 256, 0, S(st)>>>(x, q, s, y, bias, (int)M, (int)N,
+                                                                   (int)K);
     }
     return snx_launch_check("k_w8_gemv");
 }
@@ -1414,7 +1447,8 @@ size_t snx_w4a16_small_lds(size_t M, size_t K, int perm) {
     return lds;
 }
 
-// The LDS-staged kernel: M <= 4, power-of-two groups, at most 8 items/thread.
+// The streaming M = 1 kernel: group 128, K = 2048 T up to 16384, scales
+// 16-byte and qzeros 4-byte aligned.
 int snx_w4a16_gemv1_ok(size_t M, size_t K, int group, const void* scales, const void* qzeros) {
     W4Launch a{};
     a.M = (int)M;
@@ -1425,6 +1459,7 @@ int snx_w4a16_gemv1_ok(size_t M, size_t K, int group, const void* scales, const 
     return K <= 16384 && gemv1_ok(a);
 }
 
+// The LDS-staged kernel: M <= 4, power-of-two groups, at most 8 items/thread.
 int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
     return M >= 1 && M <= 4 && K % 512 == 0 && group >= 128 && (group & (group - 1)) == 0 &&
            K % (size_t)group == 0 && snx_w4a16_small_lds(M, K, perm) <= 65536 &&
@@ -1432,12 +1467,12 @@ int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
 }
 
 int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                     const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
-                     size_t N, size_t K, int group, void* st) {
+                     const uint32_t* qzeros, const uint16_t* perm, void* y, const float* bias,
+                     int y_f32, size_t M, size_t N, size_t K, int group, void* st) {
     const int G = (int)(K / (size_t)group);
     const size_t lds = snx_w4a16_small_lds(M, K, perm != NULL);
     const size_t items = M * (K / 8);
-    W4Launch a{x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, G, group, lds, S(st)};
+    W4Launch a{x, qw, scales, qzeros, perm, y, bias, y_f32, (int)M, (int)N, (int)K, G, group, lds, S(st)};
     if (gemv1_ok(a)) return perm ? launch_gemv1<true>(a) : launch_gemv1<false>(a);
     if (snx_w4a16_small_ok(M, K, group, perm != NULL)) {
         if (perm) {
@@ -1454,10 +1489,10 @@ int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scal
         return -1;
     }
     if (M <= 16)
-        return launch_w4a16<1>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+        return launch_w4a16<1>(x, qw, scales, qzeros, y, bias, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
     if (M <= 32)
-        return launch_w4a16<2>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
-    return launch_w4a16<4>(x, qw, scales, qzeros, y, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+        return launch_w4a16<2>(x, qw, scales, qzeros, y, bias, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
+    return launch_w4a16<4>(x, qw, scales, qzeros, y, bias, y_f32, (int)M, (int)N, (int)K, G, group, S(st));
 }
 
 size_t snx_w4a16_mt_lds(size_t M, size_t K, int perm) {
@@ -1470,8 +1505,8 @@ int snx_w4a16_mt_ok(size_t M, size_t K, int group, int perm) {
 }
 
 int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                        const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
-                        size_t N, size_t K, void* st) {
+                        const uint32_t* qzeros, const uint16_t* perm, void* y, const float* bias,
+                        int y_f32, size_t M, size_t N, size_t K, void* st) {
     if (!snx_w4a16_mt_ok(M, K, 128, perm != NULL)) {
         snx_set_error("w4a16 gemv: M=%zu K=%zu outside the small-M kernel", M, K);
         return -1;
@@ -1481,17 +1516,18 @@ int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* s
     const int grid = (int)(ngroups < (size_t)ncu ? ngroups : (size_t)ncu);
     const size_t lds = snx_w4a16_mt_lds(M, K, perm != NULL);
     if (perm)
-        return launch_gemv_mt_k<true>(x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, lds,
-                                      grid, S(st));
-    return launch_gemv_mt_k<false>(x, qw, scales, qzeros, perm, y, y_f32, (int)M, (int)N, (int)K, lds, grid,
-                                   S(st));
+        return launch_gemv_mt_k<true>(x, qw, scales, qzeros, perm, y, bias, y_f32, (int)M, (int)N, (int)K,
+                                      lds, grid, S(st));
+    return launch_gemv_mt_k<false>(x, qw, scales, qzeros, perm, y, bias, y_f32, (int)M, (int)N, (int)K,
+                                   lds, grid, S(st));
 }
 
 int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
-                        int y_f32, size_t M, size_t N, size_t K, int group, void* st) {
+                        const float* bias, int y_f32, size_t M, size_t N, size_t K, int group,
+                        void* st) {
     k_w4a16_generic<<<(unsigned)((N + 3) / 4), 256, 0, S(st)>>>(
-        x, qw, scales, qzeros, g_idx, y, y_f32, (int)M, (int)N, (int)K, (int)G, group);
+        x, qw, scales, qzeros, g_idx, y, bias, y_f32, (int)M, (int)N, (int)K, (int)G, group);
     return snx_launch_check("k_w4a16_generic");
 }
 

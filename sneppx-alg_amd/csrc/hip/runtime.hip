@@ -89,30 +89,41 @@ int snx_hip_free_async(void* ptr, void* stream) {
     return ptr ? check(hipFreeAsync(ptr, S(stream)), "hipFreeAsync") : 0;
 }
 
-// Workspaces kept per (device, stream, slot) for the library's internal
-// scratch (split-K partials, prepared activations, gathers).  Work on one
-// stream runs in order, so a call may reuse its stream's buffer without
+// Workspaces kept per (device, stream, slot, host thread) for the library's
+// internal scratch (split-K partials, prepared activations, gathers).  Work
+// on one stream runs in order, so a call may reuse its buffer without
 // waiting; a larger request releases the old buffer stream-ordered (after
 // the work already queued on that stream) and takes a new one from the pool.
+// Keying by thread as well means two host threads never share a buffer, even
+// when they enqueue on the same stream: one thread's stream-ordered release
+// can only follow that thread's own earlier work.  A thread's buffers live
+// until snx_release_workspaces(stream) or the end of the process.
 namespace {
 struct Workspace {
-    int dev, slot;
+    int dev, slot, thread;
     void* stream;
     void* ptr;
     size_t bytes;
 };
 std::mutex g_ws_mu;
 std::vector<Workspace> g_ws;
+std::atomic<int> g_thread_ids{0};
+
+int thread_key() {
+    thread_local int id = g_thread_ids.fetch_add(1, std::memory_order_relaxed);
+    return id;
+}
 }  // namespace
 
 void* snx_workspace(size_t bytes, int slot, void* stream) {
     int dev = 0;
     if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
     if (bytes == 0) bytes = 1;
+    const int th = thread_key();
     std::lock_guard<std::mutex> lock(g_ws_mu);
     Workspace* w = nullptr;
     for (auto& e : g_ws)
-        if (e.dev == dev && e.slot == slot && e.stream == stream) w = &e;
+        if (e.dev == dev && e.slot == slot && e.stream == stream && e.thread == th) w = &e;
     if (w && w->bytes >= bytes) return w->ptr;
     const size_t want = (bytes + (bytes >> 2) + 4095) & ~(size_t)4095;   // +25% headroom
     void* p = nullptr;
@@ -122,9 +133,25 @@ void* snx_workspace(size_t bytes, int slot, void* stream) {
         w->ptr = p;
         w->bytes = want;
     } else {
-        g_ws.push_back(Workspace{dev, slot, stream, p, want});
+        g_ws.push_back(Workspace{dev, slot, th, stream, p, want});
     }
     return p;
+}
+
+// Frees (stream-ordered) every workspace of this thread on `stream`, for a
+// caller about to destroy that stream.
+void snx_release_workspaces(void* stream) {
+    const int th = thread_key();
+    std::lock_guard<std::mutex> lock(g_ws_mu);
+    for (size_t i = 0; i < g_ws.size();) {
+        if (g_ws[i].stream == stream && g_ws[i].thread == th) {
+            (void)hipFreeAsync(g_ws[i].ptr, S(stream));
+            g_ws[i] = g_ws.back();
+            g_ws.pop_back();
+        } else {
+            i++;
+        }
+    }
 }
 
 int snx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {

@@ -116,8 +116,9 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                                                     const uint32_t* __restrict__ qw,
                                                     const uint16_t* __restrict__ scales,
                                                     const uint32_t* __restrict__ qz,
-                                                    void* __restrict__ y, int M, int N, int K,
-                                                    int G, int gshift, int Mp, int tiles_m) {
+                                                    void* __restrict__ y,
+                                                    const float* __restrict__ bias, int M, int N,
+                                                    int K, int G, int gshift, int Mp, int tiles_m) {
     // WN waves along N, 8 / WN along M: each wave owns RW rows x CW columns,
     // FM x FN blocks of 32 x 32; the result sits in FM / 2 x FN pairs of
     // blocks stacked along M (the 2-block f32 MFMA's output)
@@ -315,6 +316,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
         for (int j = 0; j < FN; j++) {
             const int n = n0 + wn * CW + j * 32 + r32;
             if (n >= N) continue;
+            const float bv = bias ? bias[n] : 0.0f;
 #pragma unroll
             for (int u = 0; u < 2; u++)
 #pragma unroll
@@ -322,9 +324,9 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                     const int m = m0 + wm * RW + 32 * (2 * i + u) + 8 * (v >> 2) + 4 * h + (v & 3);
                     if (m >= M) continue;
                     if (YF32)
-                        reinterpret_cast<float*>(y)[(size_t)m * N + n] = yq[i][j][16 * u + v];
+                        reinterpret_cast<float*>(y)[(size_t)m * N + n] = yq[i][j][16 * u + v] + bv;
                     else
-                        reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = bf16_out(yq[i][j][16 * u + v]);
+                        reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = bf16_out(yq[i][j][16 * u + v] + bv);
                 }
         }
     }
@@ -332,8 +334,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
 
 template <bool ZEROS, bool YF32, int WN>
 int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
-                   const uint16_t* scales, const uint32_t* qz, void* y, int M, int N, int K,
-                   int group, int Mp, hipStream_t st) {
+                   const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
+                   int N, int K, int group, int Mp, hipStream_t st) {
     const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
     const size_t lds = (size_t)GSTAGES * GRING;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
@@ -344,7 +346,7 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
     }
     const int gshift = __builtin_ctz((unsigned)group);
     k_w4a16_gemm<ZEROS, YF32, WN><<<tiles_m * tiles_n, 512, lds, st>>>(
-        xp, xs, qw, scales, qz, y, M, N, K, K / group, gshift, Mp, tiles_m);
+        xp, xs, qw, scales, qz, y, bias, M, N, K, K / group, gshift, Mp, tiles_m);
     return snx_launch_check("k_w4a16_gemm");
 }
 
@@ -474,15 +476,15 @@ int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t
 }
 
 int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
-                     const uint16_t* scales, const uint32_t* qzeros, void* y, int y_f32,
-                     size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
+                     const uint16_t* scales, const uint32_t* qzeros, void* y, const float* bias,
+                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
     const int m = (int)M, n = (int)N, k = (int)K, mp = (int)Mp;
     if (qzeros) {
-        if (y_f32) return launch_w4_gemm<true, true, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
-        return launch_w4_gemm<true, false, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+        if (y_f32) return launch_w4_gemm<true, true, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+        return launch_w4_gemm<true, false, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
     }
-    if (y_f32) return launch_w4_gemm<false, true, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
-    return launch_w4_gemm<false, false, W4_WN>(xp, xs, qw, scales, qzeros, y, m, n, k, group, mp, S(st));
+    if (y_f32) return launch_w4_gemm<false, true, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+    return launch_w4_gemm<false, false, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
 }
 
 }  // extern "C"

@@ -12,9 +12,8 @@
 #include "snx_hip.h"
 #include "../snx_internal.h"
 
-/* workspace slots of this file (qlinear.c uses 0 and 1 inside the linears) */
+/* workspace slot of this file (qlinear.c uses 0 and 1 inside the linears) */
 #define SLOT_X_BF16 2
-#define SLOT_HOST_IO 3
 
 struct SNEPPXQLayer {
     int format;
@@ -30,6 +29,7 @@ struct SNEPPXQLayer {
     int32_t* g_idx;       /* NULL: contiguous groups */
     uint32_t* qsorted;    /* act-order prepared (group-contiguous) codes, or NULL */
     uint16_t* perm;
+    float* bias;          /* fp32 [N] or NULL */
 };
 
 void SNEPPX_qlayer_destroy(SNEPPXQLayer* L) {
@@ -42,7 +42,47 @@ void SNEPPX_qlayer_destroy(SNEPPXQLayer* L) {
     snx_hip_free(L->g_idx);
     snx_hip_free(L->qsorted);
     snx_hip_free(L->perm);
+    snx_hip_free(L->bias);
     free(L);
+}
+
+static int set_bias(SNEPPXQLayer* L, const float* b, int on_device, SNEPPXStream stream) {
+    if (!L) { snx_set_error("qlayer_set_bias: NULL layer"); return -1; }
+    snx_clear_error();
+    if (!b) {
+        snx_hip_free(L->bias);
+        L->bias = NULL;
+        return 0;
+    }
+    if (!L->bias && snx_hip_malloc((void**)&L->bias, L->N * sizeof(float))) return -1;
+    int rc = on_device ? snx_hip_memcpy_d2d(L->bias, b, L->N * sizeof(float), stream)
+                       : snx_hip_memcpy_h2d(L->bias, b, L->N * sizeof(float), stream);
+    if (!rc && !on_device) rc = snx_hip_stream_sync(stream);   /* the host buffer may go away */
+    return rc;
+}
+
+int SNEPPX_qlayer_set_bias(SNEPPXQLayer* L, const float* bias, SNEPPXStream stream) {
+    return set_bias(L, bias, 0, stream);
+}
+
+int SNEPPX_qlayer_set_bias_device(SNEPPXQLayer* L, const float* d_bias, SNEPPXStream stream) {
+    return set_bias(L, d_bias, 1, stream);
+}
+
+/* <prefix>.bias: F32 [N] when present (written by SNEPPX_qlayer_save) */
+static int load_bias(SNEPPXQLayer* L, const SNEPPXQStore* st, const char* prefix,
+                     SNEPPXStream stream) {
+    char key[512];
+    snprintf(key, sizeof key, "%s.bias", prefix);
+    int dt;
+    size_t shape[SNEPPX_QST_MAX_DIMS], nd, nb;
+    if (SNEPPX_qstore_info(st, key, &dt, shape, &nd, &nb)) return 0;   /* no bias */
+    if (dt != SNEPPX_QST_F32 || nd != 1 || shape[0] != L->N) {
+        snx_set_error("qlayer_load: %s must be F32 [%zu]", key, L->N);
+        return -1;
+    }
+    if (snx_hip_malloc((void**)&L->bias, L->N * sizeof(float))) return -1;
+    return SNEPPX_qstore_read_device(st, key, L->bias, L->N * sizeof(float), stream);
 }
 
 size_t SNEPPX_qlayer_in_features(const SNEPPXQLayer* L) { return L ? L->K : 0; }
@@ -154,7 +194,8 @@ SNEPPXQLayer* SNEPPX_qlayer_load(const SNEPPXQStore* st, const char* prefix, SNE
         if (SNEPPX_qstore_query_w8(st, prefix, &N, &K)) return NULL;
         SNEPPXQLayer* L = alloc_layer(SNEPPX_QLAYER_W8, K, N, 0, 0, 0, 0);
         if (!L) return NULL;
-        if (SNEPPX_qstore_load_w8(st, prefix, L->q8, L->s8, stream)) {
+        if (SNEPPX_qstore_load_w8(st, prefix, L->q8, L->s8, stream) ||
+            load_bias(L, st, prefix, stream)) {
             SNEPPX_qlayer_destroy(L);
             return NULL;
         }
@@ -165,7 +206,8 @@ SNEPPXQLayer* SNEPPX_qlayer_load(const SNEPPXQStore* st, const char* prefix, SNE
         if (!fmt && SNEPPX_qstore_query_w8(st, prefix, &N, &K) == 0) {   /* W8 without metadata */
             SNEPPXQLayer* L = alloc_layer(SNEPPX_QLAYER_W8, K, N, 0, 0, 0, 0);
             if (!L) return NULL;
-            if (SNEPPX_qstore_load_w8(st, prefix, L->q8, L->s8, stream)) {
+            if (SNEPPX_qstore_load_w8(st, prefix, L->q8, L->s8, stream) ||
+                load_bias(L, st, prefix, stream)) {
                 SNEPPX_qlayer_destroy(L);
                 return NULL;
             }
@@ -180,7 +222,7 @@ SNEPPXQLayer* SNEPPX_qlayer_load(const SNEPPXQStore* st, const char* prefix, SNE
     SNEPPXQLayer* L = alloc_layer(SNEPPX_QLAYER_W4, K, N, hg ? 0 : group, G, hz, hg);
     if (!L) return NULL;
     if (SNEPPX_qstore_load_w4(st, prefix, L->qweight, L->scales, L->qzeros, L->g_idx, stream) ||
-        try_prepare(L, stream)) {
+        load_bias(L, st, prefix, stream) || try_prepare(L, stream)) {
         SNEPPX_qlayer_destroy(L);
         return NULL;
     }
@@ -190,20 +232,27 @@ SNEPPXQLayer* SNEPPX_qlayer_load(const SNEPPXQStore* st, const char* prefix, SNE
 int SNEPPX_qlayer_save(const SNEPPXQLayer* L, SNEPPXQStoreWriter* w, const char* prefix,
                        SNEPPXStream stream) {
     if (!L || !w || !prefix) { snx_set_error("qlayer_save: NULL argument"); return -1; }
-    if (L->format == SNEPPX_QLAYER_W8)
-        return SNEPPX_qstore_save_w8(w, prefix, L->q8, L->s8, L->N, L->K, stream);
-    return SNEPPX_qstore_save_w4(w, prefix, L->qweight, L->scales, L->qzeros, L->g_idx, L->N, L->K,
-                                 L->group, L->G, stream);
+    int rc = L->format == SNEPPX_QLAYER_W8
+                 ? SNEPPX_qstore_save_w8(w, prefix, L->q8, L->s8, L->N, L->K, stream)
+                 : SNEPPX_qstore_save_w4(w, prefix, L->qweight, L->scales, L->qzeros, L->g_idx,
+                                         L->N, L->K, L->group, L->G, stream);
+    if (!rc && L->bias) {
+        char key[512];
+        snprintf(key, sizeof key, "%s.bias", prefix);
+        const size_t shape[1] = {L->N};
+        rc = SNEPPX_qstore_writer_add_device(w, key, SNEPPX_QST_F32, shape, 1, L->bias, stream);
+    }
+    return rc;
 }
 
 /* W4A16 with bf16 activations, output in y_dtype */
 static int run_w4(const SNEPPXQLayer* L, const uint16_t* xb, void* y, SNEPPXDtype ydt, size_t M,
                   SNEPPXStream stream) {
     if (L->qsorted)   /* act-order, prepared: groups of K/G sorted columns */
-        return SNEPPX_qlinear_w4a16_actorder(xb, L->qsorted, L->scales, L->qzeros, L->perm, y, ydt, M,
-                                             L->N, L->K, (int)(L->K / L->G), stream);
-    return SNEPPX_qlinear_w4a16(xb, L->qweight, L->scales, L->qzeros, L->g_idx, L->G, y, ydt, M,
-                                L->N, L->K, L->group, stream);
+        return SNEPPX_qlinear_w4a16_actorder(xb, L->qsorted, L->scales, L->qzeros, L->perm, L->bias,
+                                             y, ydt, M, L->N, L->K, (int)(L->K / L->G), stream);
+    return SNEPPX_qlinear_w4a16(xb, L->qweight, L->scales, L->qzeros, L->g_idx, L->G, L->bias, y,
+                                ydt, M, L->N, L->K, L->group, stream);
 }
 
 int SNEPPX_qlayer_forward_f32(const SNEPPXQLayer* L, const float* d_x, float* d_y, size_t M,
@@ -212,7 +261,7 @@ int SNEPPX_qlayer_forward_f32(const SNEPPXQLayer* L, const float* d_x, float* d_
     if (!M) { snx_set_error("qlayer_forward_f32: M = 0"); return -1; }
     snx_clear_error();
     if (L->format == SNEPPX_QLAYER_W8)
-        return SNEPPX_qlinear_w8_gemv(d_x, L->q8, L->s8, d_y, M, L->N, L->K, stream);
+        return SNEPPX_qlinear_w8_gemv(d_x, L->q8, L->s8, L->bias, d_y, M, L->N, L->K, stream);
     uint16_t* xb = (uint16_t*)snx_workspace(M * L->K * 2, SLOT_X_BF16, stream);
     if (!xb) return -1;
     if (snx_k_f32_to_bf16(d_x, xb, M * L->K, stream)) return -1;
@@ -231,16 +280,26 @@ int SNEPPX_qlayer_forward_bf16(const SNEPPXQLayer* L, const uint16_t* d_x, uint1
     return run_w4(L, d_x, d_y, SNEPPX_BFLOAT16, M, stream);
 }
 
+/* Each call owns its stream and its staging (stream-ordered allocations from
+ * the device pool), so concurrent calls share no buffer: the workspaces the
+ * linears take inside are keyed by (thread, stream) and this stream is the
+ * call's own. */
 int SNEPPX_qlayer_matmul_host(const SNEPPXQLayer* L, const float* x, float* y, size_t M) {
     if (!L || !x || !y || !M) { snx_set_error("qlayer_matmul_host: NULL or empty argument"); return -1; }
     const size_t xb = M * L->K * 4, yb = M * L->N * 4;
-    const size_t xoff = (yb + 255) & ~(size_t)255;
-    char* ws = (char*)snx_workspace(xoff + xb, SLOT_HOST_IO, NULL);
-    if (!ws) return -1;
-    float* dy = (float*)ws;
-    float* dx = (float*)(ws + xoff);
-    if (snx_hip_memcpy_h2d(dx, x, xb, NULL) || SNEPPX_qlayer_forward_f32(L, dx, dy, M, NULL) ||
-        snx_hip_memcpy_d2h(y, dy, yb, NULL))
-        return -1;
-    return snx_hip_stream_sync(NULL);
+    void* st = NULL;
+    if (snx_hip_stream_create(&st)) return -1;
+    float* dx = NULL;
+    float* dy = NULL;
+    int rc = snx_hip_malloc_async((void**)&dx, xb, st);
+    if (!rc) rc = snx_hip_malloc_async((void**)&dy, yb, st);
+    if (!rc) rc = snx_hip_memcpy_h2d(dx, x, xb, st);
+    if (!rc) rc = SNEPPX_qlayer_forward_f32(L, dx, dy, M, st);
+    if (!rc) rc = snx_hip_memcpy_d2h(y, dy, yb, st);
+    snx_hip_free_async(dx, st);
+    snx_hip_free_async(dy, st);
+    const int rs = snx_hip_stream_sync(st);
+    snx_release_workspaces(st);
+    snx_hip_stream_destroy(st);
+    return rc || rs ? -1 : 0;
 }

@@ -104,20 +104,21 @@ int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* sc
     return rc;
 }
 
-int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* scales, float* y,
-                           size_t M, size_t N, size_t K, SNEPPXStream stream) {
+int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* scales,
+                           const float* bias, float* y, size_t M, size_t N, size_t K,
+                           SNEPPXStream stream) {
     REQUIRE(x && qweight && scales && y, "qlinear_w8_gemv: NULL pointer");
     REQUIRE(M && N && K, "qlinear_w8_gemv: empty shape");
     REQUIRE(K % 16 != 0 || (aligned16(x) && aligned16(qweight)),
             "qlinear_w8_gemv: x and qweight must be 16-byte aligned");
     snx_clear_error();
-    return snx_k_w8_gemv(x, qweight, scales, y, M, N, K, stream);
+    return snx_k_w8_gemv(x, qweight, scales, y, bias, M, N, K, stream);
 }
 
 int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
-                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
-                         SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
-                         SNEPPXStream stream) {
+                         const uint32_t* qzeros, const int32_t* g_idx, size_t G,
+                         const float* bias, void* y, SNEPPXDtype y_dtype, size_t M, size_t N,
+                         size_t K, int group, SNEPPXStream stream) {
     REQUIRE(x && qweight && scales && y, "qlinear_w4a16: NULL pointer");
     REQUIRE(M && N && K, "qlinear_w4a16: empty shape");
     REQUIRE(K % 8 == 0, "qlinear_w4a16: K=%zu must be a multiple of 8", K);
@@ -143,14 +144,14 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         uint16_t* xp = (uint16_t*)ws;
         float* xs = (float*)(ws + xp_bytes);
         int rc = snx_k_w4_prep_x(x, xp, xs, M, K, Mp, stream);
-        if (!rc) rc = snx_k_w4a16_gemm(xp, xs, qweight, scales, qzeros, y, y_f32, M, N, K, group,
-                                       Mp, stream);
+        if (!rc) rc = snx_k_w4a16_gemm(xp, xs, qweight, scales, qzeros, y, bias, y_f32, M, N, K,
+                                       group, Mp, stream);
         return rc;
     }
     if (!g_idx && snx_w4a16_mt_ok(M, K, group, 0) && aligned16(x) && aligned16(qweight) &&
         ((uintptr_t)scales & 3u) == 0 && ((uintptr_t)qzeros & 3u) == 0) {
         /* 2 <= M <= 16: one persistent workgroup per CU, activations staged once */
-        return snx_k_w4a16_gemv_mt(x, qweight, scales, qzeros, NULL, y, y_f32, M, N, K, stream);
+        return snx_k_w4a16_gemv_mt(x, qweight, scales, qzeros, NULL, y, bias, y_f32, M, N, K, stream);
     }
     const int kspan = snx_w4a16_splitk_span(M, K, group);
     if (!g_idx && (M > 4 || (M > 1 && !snx_w4a16_small_ok(M, K, group, 0))) && kspan &&
@@ -161,7 +162,7 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         float* part = (float*)snx_workspace(S * M * N * sizeof(float), 1, stream);
         if (!part) return -1;
         int rc = snx_k_w4a16_splitk(x, qweight, scales, qzeros, part, M, N, K, group, kspan, stream);
-        if (!rc) rc = snx_k_w4a16_reduce(part, y, y_f32, (int)S, M * N, stream);
+        if (!rc) rc = snx_k_w4a16_reduce(part, y, y_f32, (int)S, M * N, N, bias, stream);
         return rc;
     }
     if (!g_idx && aligned16(x) && aligned16(qweight) &&
@@ -171,13 +172,13 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         for (size_t m0 = 0; m0 < M; m0 += 64) {
             size_t mm = M - m0 < 64 ? M - m0 : 64;
             if (snx_k_w4a16_gemv(x + m0 * K, qweight, scales, qzeros, NULL,
-                                 (char*)y + m0 * N * ob, y_f32, mm, N, K, group, stream))
+                                 (char*)y + m0 * N * ob, bias, y_f32, mm, N, K, group, stream))
                 return -1;
         }
         return 0;
     }
-    return snx_k_w4a16_generic(x, qweight, scales, qzeros, g_idx, G, y, y_f32, M, N, K, group,
-                               stream);
+    return snx_k_w4a16_generic(x, qweight, scales, qzeros, g_idx, G, y, bias, y_f32, M, N, K,
+                               group, stream);
 }
 
 /* Stable counting sort of g_idx on the host (one small copy each way). */
@@ -221,8 +222,9 @@ int SNEPPX_qlinear_w4_actorder_prepare(const uint32_t* qweight, const int32_t* g
 
 int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sorted,
                                   const uint16_t* scales, const uint32_t* qzeros,
-                                  const uint16_t* perm, void* y, SNEPPXDtype y_dtype, size_t M,
-                                  size_t N, size_t K, int group, SNEPPXStream stream) {
+                                  const uint16_t* perm, const float* bias, void* y,
+                                  SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
+                                  SNEPPXStream stream) {
     REQUIRE(x && qweight_sorted && scales && perm && y, "qlinear_w4a16_actorder: NULL pointer");
     REQUIRE(M && N && K, "qlinear_w4a16_actorder: empty shape");
     REQUIRE(K % 8 == 0 && K <= 65536, "qlinear_w4a16_actorder: K=%zu must be a multiple of 8 and <= 65536", K);
@@ -233,18 +235,18 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
     snx_clear_error();
     if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) && ((uintptr_t)scales & 3u) == 0 &&
         ((uintptr_t)qzeros & 3u) == 0 && snx_w4a16_mt_ok(M, K, group, 1))
-        return snx_k_w4a16_gemv_mt(x, qweight_sorted, scales, qzeros, perm, y, y_dtype == SNEPPX_FLOAT32,
-                                   M, N, K, stream);
+        return snx_k_w4a16_gemv_mt(x, qweight_sorted, scales, qzeros, perm, y, bias,
+                                   y_dtype == SNEPPX_FLOAT32, M, N, K, stream);
     if (aligned16(x) && aligned16(qweight_sorted) && aligned16(perm) &&
         (snx_w4a16_small_ok(M, K, group, 1) || snx_w4a16_gemv1_ok(M, K, group, scales, qzeros)))
-        return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y,
+        return snx_k_w4a16_gemv(x, qweight_sorted, scales, qzeros, perm, y, bias,
                                 y_dtype == SNEPPX_FLOAT32, M, N, K, group, stream);
     /* other shapes: gather the activation columns once, then the plain path */
     uint16_t* xs = (uint16_t*)snx_workspace(M * K * sizeof(uint16_t), 0, stream);
     if (!xs) return -1;
     int rc = snx_k_gather_cols(x, perm, xs, M, K, stream);
-    if (!rc) rc = SNEPPX_qlinear_w4a16(xs, qweight_sorted, scales, qzeros, NULL, 0, y, y_dtype,
-                                       M, N, K, group, stream);
+    if (!rc) rc = SNEPPX_qlinear_w4a16(xs, qweight_sorted, scales, qzeros, NULL, 0, bias, y,
+                                       y_dtype, M, N, K, group, stream);
     return rc;
 }
 
@@ -278,12 +280,13 @@ int SNEPPX_dev_quantize_int8_channel_bf16(const uint16_t* in, int8_t* q, float* 
 }
 
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,
-                           uint16_t* out, size_t M, size_t N, size_t K, SNEPPXStream stream) {
+                           const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                           SNEPPXStream stream) {
     REQUIRE(A && sA && W && sW && out, "qlinear_w8a8_i8: NULL pointer");
     REQUIRE(M && N && K, "qlinear_w8a8_i8: empty shape");
     REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_i8: A and W must be 16-byte aligned");
     snx_clear_error();
-    return snx_k_i8_gemm(A, W, sA, sW, NULL, out, M, N, K, stream);
+    return snx_k_i8_gemm(A, W, sA, sW, NULL, out, bias, M, N, K, stream);
 }
 
 int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C, size_t M, size_t N,
@@ -292,14 +295,15 @@ int SNEPPX_qlinear_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C, siz
     REQUIRE(M && N && K, "qlinear_i8_gemm_i32: empty shape");
     REQUIRE(aligned16(A) && aligned16(W), "qlinear_i8_gemm_i32: A and W must be 16-byte aligned");
     snx_clear_error();
-    return snx_k_i8_gemm(A, W, NULL, NULL, C, NULL, M, N, K, stream);
+    return snx_k_i8_gemm(A, W, NULL, NULL, C, NULL, NULL, M, N, K, stream);
 }
 
 int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W, const float* sW,
-                            uint16_t* out, size_t M, size_t N, size_t K, SNEPPXStream stream) {
+                            const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                            SNEPPXStream stream) {
     REQUIRE(A && sA && W && sW && out, "qlinear_w8a8_fp8: NULL pointer");
     REQUIRE(M && N && K, "qlinear_w8a8_fp8: empty shape");
     REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_fp8: A and W must be 16-byte aligned");
     snx_clear_error();
-    return snx_k_fp8_gemm(A, W, sA, sW, out, M, N, K, stream);
+    return snx_k_fp8_gemm(A, W, sA, sW, out, bias, M, N, K, stream);
 }

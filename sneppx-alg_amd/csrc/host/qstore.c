@@ -11,6 +11,7 @@
 #define _GNU_SOURCE
 #include <errno.h>
 #include <fcntl.h>
+#include <limits.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -343,6 +344,7 @@ SNEPPXQStore* SNEPPX_qstore_open(const char* path) {
                 if (e->shape[d] && cnt > SIZE_MAX / e->shape[d]) FAIL("qstore_open: %s shape overflows", e->name);
                 cnt *= e->shape[d];
             }
+            if (cnt > SIZE_MAX / k_dtype_size[e->dtype]) FAIL("qstore_open: %s byte size overflows", e->name);
             if (cnt * k_dtype_size[e->dtype] != e->end - e->begin)
                 FAIL("qstore_open: %s holds %zu bytes, its dtype and shape need %zu", e->name,
                      e->end - e->begin, cnt * k_dtype_size[e->dtype]);
@@ -737,10 +739,17 @@ int SNEPPX_qstore_query_w4(const SNEPPXQStore* st, const char* prefix, size_t* N
     int rz = tensor2(st, prefix, "qzeros", SNEPPX_QST_I32, 2, qz);
     int rg = tensor2(st, prefix, "g_idx", SNEPPX_QST_I32, 1, gi);
     if (rz < 0 || rg < 0) return -1;
+    /* every tensor's byte count matched its data_offsets at open, so N K / 2
+     * and N G 2 fit in size_t; the kernels also index rows and columns with
+     * int */
     size_t n = qw[0], k = qw[1] * 8, g = sc[1];
     if (!n || !k || !g || sc[0] != n || (rz == 0 && (qz[0] != n || qz[1] != (g + 7) / 8)) ||
         (rg == 0 && gi[0] != k) || (rg != 0 && k % g)) {
         snx_set_error("qstore_query_w4: %s tensors have inconsistent shapes", prefix);
+        return -1;
+    }
+    if (n > INT_MAX || qw[1] > INT_MAX / 8 || g > INT_MAX) {
+        snx_set_error("qstore_query_w4: %s has N=%zu, K=%zu beyond the kernels' int range", prefix, n, k);
         return -1;
     }
     if (N) *N = n;
@@ -804,6 +813,11 @@ int SNEPPX_qstore_query_w8(const SNEPPXQStore* st, const char* prefix, size_t* N
     if (r) { if (r > 0) snx_set_error("qstore_query_w8: no %s.weight_scale", prefix); return -1; }
     if (!q[0] || !q[1] || s[0] != q[0]) {
         snx_set_error("qstore_query_w8: %s tensors have inconsistent shapes", prefix);
+        return -1;
+    }
+    if (q[0] > INT_MAX || q[1] > INT_MAX) {
+        snx_set_error("qstore_query_w8: %s has N=%zu, K=%zu beyond the kernels' int range", prefix,
+                      q[0], q[1]);
         return -1;
     }
     if (N) *N = q[0];

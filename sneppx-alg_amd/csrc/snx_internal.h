@@ -15,9 +15,12 @@ extern "C" {
 #endif
 
 void snx_set_error(const char* fmt, ...);
-/* device scratch reused by every call on (current device, stream, slot);
- * slot 1 is for a call made from inside another one.  NULL on failure. */
+/* device scratch reused by every call on (current device, stream, slot) from
+ * the calling host thread; slot 1 is for a call made from inside another
+ * one.  NULL on failure. */
 void* snx_workspace(size_t bytes, int slot, void* stream);
+/* stream-ordered release of the calling thread's workspaces on `stream` */
+void snx_release_workspaces(void* stream);
 void snx_clear_error(void);
 int snx_launch_check(const char* kernel);
 
@@ -103,13 +106,14 @@ int snx_k_w4_gptq_quantize(const float* w, const int32_t* g_idx, size_t G, uint3
                            uint16_t* scales, size_t N, size_t K, void* stream);
 
 /* ---- linears (gemv_kernels.hip, gemm_kernels.hip) ---- */
-int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y,
+/* bias (fp32 [N] or NULL) is added to the fp32 result of every linear below */
+int snx_k_w8_gemv(const float* x, const int8_t* q, const float* s, float* y, const float* bias,
                   size_t M, size_t N, size_t K, void* stream);
 /* y_f32: 1 -> fp32 output, 0 -> bf16.  perm (uint16 [K], may be NULL): the
  * weight columns are stored in that order (M <= 4 only, see small_ok). */
 int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                     const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32,
-                     size_t M, size_t N, size_t K, int group, void* stream);
+                     const uint32_t* qzeros, const uint16_t* perm, void* y, const float* bias,
+                     int y_f32, size_t M, size_t N, size_t K, int group, void* stream);
 size_t snx_w4a16_small_lds(size_t M, size_t K, int perm);
 int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm);
 /* the M = 1 streaming decode kernel applies (group 128, K = 2048 T <= 16384,
@@ -121,7 +125,8 @@ int snx_w4a16_splitk_span(size_t M, size_t K, int group);
 int snx_k_w4a16_splitk(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
                        const uint32_t* qzeros, float* part, size_t M, size_t N, size_t K,
                        int group, int kspan, void* stream);
-int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S, size_t MN, void* stream);
+int snx_k_w4a16_reduce(const float* part, void* y, int y_f32, int S, size_t MN, size_t N,
+                       const float* bias, void* stream);
 /* xs[m][k'] = x[m][perm[k']] (bf16), perm entries < K */
 int snx_k_gather_cols(const uint16_t* x, const uint16_t* perm, uint16_t* xs, size_t M, size_t K,
                       void* stream);
@@ -134,11 +139,12 @@ int snx_k_w4_permute_cols(const uint32_t* qw, const uint16_t* perm, uint32_t* qs
 size_t snx_w4a16_mt_lds(size_t M, size_t K, int perm);
 int snx_w4a16_mt_ok(size_t M, size_t K, int group, int perm);
 int snx_k_w4a16_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
-                        const uint32_t* qzeros, const uint16_t* perm, void* y, int y_f32, size_t M,
-                        size_t N, size_t K, void* stream);
+                        const uint32_t* qzeros, const uint16_t* perm, void* y, const float* bias,
+                        int y_f32, size_t M, size_t N, size_t K, void* stream);
 int snx_k_w4a16_generic(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
                         const uint32_t* qzeros, const int32_t* g_idx, size_t G, void* y,
-                        int y_f32, size_t M, size_t N, size_t K, int group, void* stream);
+                        const float* bias, int y_f32, size_t M, size_t N, size_t K, int group,
+                        void* stream);
 int snx_w4a16_gemv_supported(size_t M, size_t N, size_t K, int group);
 
 /* W4A16 prefill GEMM (w4_gemm_kernels.hip): activations prepared once
@@ -148,8 +154,8 @@ int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group);
 int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,
                     void* stream);
 int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
-                     const uint16_t* scales, const uint32_t* qzeros, void* y, int y_f32,
-                     size_t M, size_t N, size_t K, int group, size_t Mp, void* stream);
+                     const uint16_t* scales, const uint32_t* qzeros, void* y, const float* bias,
+                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, void* stream);
 
 /* SwiGLU step: out [T][F] = bf16(silu(gu[:, :F]) * gu[:, F:]), F % 8 == 0 */
 /* SwiGLU then per-token int8 of the bf16 result (F % 8 == 0, F <= 32768) */
@@ -158,10 +164,11 @@ int snx_k_silu_mul_quant_int8(const uint16_t* gu, int8_t* q, float* scales, size
 int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* stream);
 
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
-                  int32_t* c_i32, uint16_t* out_bf16, size_t M, size_t N, size_t K,
-                  void* stream);
+                  int32_t* c_i32, uint16_t* out_bf16, const float* bias, size_t M, size_t N,
+                  size_t K, void* stream);
 int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const float* sW,
-                   uint16_t* out_bf16, size_t M, size_t N, size_t K, void* stream);
+                   uint16_t* out_bf16, const float* bias, size_t M, size_t N, size_t K,
+                   void* stream);
 
 #ifdef __cplusplus
 }

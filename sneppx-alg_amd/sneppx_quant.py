@@ -70,18 +70,18 @@ EXPORTS = {
     "SNEPPX_dev_quantize_w4_awq": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp]),
     "SNEPPX_dev_quantize_w4_gptq": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_fp8_e4m3_scaled": (C.c_int, [_vp, _vp, _vp, _sz, _vp]),
-    "SNEPPX_qlinear_w8_gemv": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
-    "SNEPPX_qlinear_w4a16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, C.c_int, _sz, _sz, _sz,
-                                       C.c_int, _vp]),
+    "SNEPPX_qlinear_w8_gemv": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w4a16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, C.c_int, _sz, _sz,
+                                       _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_w4_actorder_prepare": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
-    "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz,
-                                                C.c_int, _vp]),
+    "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz,
+                                                _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_silu_mul_quant_int8": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_int8_channel_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
-    "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_i8_gemm_i32": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _sz, _vp]),
-    "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w8a8_fp8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     # quantized weights on disk + model-zoo int8 (include/sneppx_qstore.h)
     "SNEPPX_qstore_open": (_vp, [C.c_char_p]),
     "SNEPPX_qstore_close": (None, [_vp]),
@@ -115,6 +115,8 @@ EXPORTS = {
     "SNEPPX_qlayer_load": (_vp, [_vp, C.c_char_p, _vp]),
     "SNEPPX_qlayer_save": (C.c_int, [_vp, _vp, C.c_char_p, _vp]),
     "SNEPPX_qlayer_destroy": (None, [_vp]),
+    "SNEPPX_qlayer_set_bias": (C.c_int, [_vp, _f32p, _vp]),
+    "SNEPPX_qlayer_set_bias_device": (C.c_int, [_vp, _vp, _vp]),
     "SNEPPX_qlayer_in_features": (_sz, [_vp]),
     "SNEPPX_qlayer_out_features": (_sz, [_vp]),
     "SNEPPX_qlayer_format": (C.c_int, [_vp]),
@@ -324,19 +326,20 @@ class Library:
         self.check(self.fn["SNEPPX_dev_quantize_fp8_e4m3_scaled"](
             _ptr(x), _ptr(out), _ptr(scale), x.numel(), self._stream(stream)), "dev_quantize_fp8_e4m3_scaled")
 
-    def qlinear_w8_gemv(self, x, qweight, scales, y, stream=None):
+    def qlinear_w8_gemv(self, x, qweight, scales, y, stream=None, bias=None):
         M, K = x.shape
         N = qweight.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8_gemv"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(y), M, N, K, self._stream(stream)), "qlinear_w8_gemv")
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(bias), _ptr(y), M, N, K, self._stream(stream)),
+            "qlinear_w8_gemv")
 
-    def qlinear_w4a16(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None):
+    def qlinear_w4a16(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None, bias=None):
         M, K = x.shape
         N = qweight.shape[0]
         ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
         self.check(self.fn["SNEPPX_qlinear_w4a16"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(y), ydt,
-            M, N, K, group, self._stream(stream)), "qlinear_w4a16")
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(bias), _ptr(y),
+            ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16")
 
     def qlinear_w4_actorder_prepare(self, qweight, g_idx, G, qweight_sorted, perm, stream=None):
         N, K8 = qweight.shape
@@ -344,13 +347,14 @@ class Library:
             _ptr(qweight), _ptr(g_idx), G, _ptr(qweight_sorted), _ptr(perm), N, K8 * 8,
             self._stream(stream)), "qlinear_w4_actorder_prepare")
 
-    def qlinear_w4a16_actorder(self, x, qweight_sorted, scales, qzeros, perm, y, group, stream=None):
+    def qlinear_w4a16_actorder(self, x, qweight_sorted, scales, qzeros, perm, y, group, stream=None,
+                               bias=None):
         M, K = x.shape
         N = qweight_sorted.shape[0]
         ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
         self.check(self.fn["SNEPPX_qlinear_w4a16_actorder"](
-            _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(y), ydt,
-            M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
+            _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(bias), _ptr(y),
+            ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
 
     def qlinear_silu_mul(self, gate_up, out, stream=None):
         T, F2 = gate_up.shape
@@ -369,11 +373,12 @@ class Library:
             _ptr(x), _ptr(q), _ptr(scales), rows, cols, self._stream(stream)),
             "dev_quantize_int8_channel_bf16")
 
-    def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None):
+    def qlinear_w8a8_i8(self, A, sA, W, sW, out, stream=None, bias=None):
         M, K = A.shape
         N = W.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8a8_i8"](
-            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), M, N, K, self._stream(stream)), "qlinear_w8a8_i8")
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(bias), _ptr(out), M, N, K, self._stream(stream)),
+            "qlinear_w8a8_i8")
 
     def qlinear_i8_gemm_i32(self, A, W, Cm, stream=None):
         M, K = A.shape
@@ -381,11 +386,12 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_i8_gemm_i32"](
             _ptr(A), _ptr(W), _ptr(Cm), M, N, K, self._stream(stream)), "qlinear_i8_gemm_i32")
 
-    def qlinear_w8a8_fp8(self, A, sA, W, sW, out, stream=None):
+    def qlinear_w8a8_fp8(self, A, sA, W, sW, out, stream=None, bias=None):
         M, K = A.shape
         N = W.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8a8_fp8"](
-            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), M, N, K, self._stream(stream)), "qlinear_w8a8_fp8")
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(bias), _ptr(out), M, N, K, self._stream(stream)),
+            "qlinear_w8a8_fp8")
 
     # ---------------- model-zoo int8 (weights.c:225-252) -------------------
     def quantize_int8_modelzoo(self, x):
@@ -654,6 +660,17 @@ class QLayer:
         M = x.shape[0]
         self.L.check(self.L.fn["SNEPPX_qlayer_forward_bf16"](self.h, _ptr(x), _ptr(y), M,
                                                              self.L._stream(stream)), "qlayer_forward_bf16")
+
+    def set_bias(self, bias, stream=None):
+        """bias: numpy fp32 [N] (host), a torch fp32 [N] device tensor, or None."""
+        if bias is None:
+            rc = self.L.fn["SNEPPX_qlayer_set_bias_device"](self.h, None, self.L._stream(stream))
+        elif isinstance(bias, np.ndarray):
+            rc = self.L.fn["SNEPPX_qlayer_set_bias"](self.h, np.ascontiguousarray(bias, np.float32),
+                                                      self.L._stream(stream))
+        else:
+            rc = self.L.fn["SNEPPX_qlayer_set_bias_device"](self.h, _ptr(bias), self.L._stream(stream))
+        self.L.check(rc, "qlayer_set_bias")
 
     def matmul_host(self, x):
         x = np.ascontiguousarray(x, np.float32)

@@ -95,23 +95,32 @@ def test_lm_head_shape_and_device_weight(lib, oracle):
     assert rel_err(got, yo) <= 1e-2
 
 
-def test_loaded_actorder_layer_is_prepared_and_exact(lib, oracle, tmp_path):
-    K, N, M = 2048, 512, 3
-    rng = np.random.default_rng(8)
+@pytest.mark.parametrize("M,zeros", [(3, False), (1, True), (8, True)])
+def test_loaded_actorder_layer_is_prepared_and_exact(lib, oracle, tmp_path, M, zeros):
+    # GPTQ act-order files with and without zero points (qzeros [N][G/8]):
+    # loading prepares them, and M = 1 / 8 run the prepared decode kernels
+    K, N = 2048, 512
+    rng = np.random.default_rng(8 + M)
     g_idx = (rng.permutation(K) // 128).astype(np.int32)
     w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
     rc, qw, sc = oracle.w4_gptq_quantize(w, g_idx, 16)
+    qz = None
+    if zeros:
+        z = rng.integers(0, 16, (N, 16)).astype(np.uint32)
+        qz = (z.reshape(N, 2, 8) << (4 * np.arange(8, dtype=np.uint32))).sum(-1).astype(np.uint32)
     path = str(tmp_path / "gptq.safetensors")
     wr = lib.qstore_writer(path)
     wr.add_host("g.qweight", "I32", qw.view(np.int32))
     wr.add_host("g.scales", "F16", sc.view(np.float16))
     wr.add_host("g.g_idx", "I32", g_idx)
+    if zeros:
+        wr.add_host("g.qzeros", "I32", qz.view(np.int32))
     wr.close()
     with lib.qstore_open(path) as st:
         layer = lib.qlayer_load(st, "g")
     x = rng.normal(0, 1, (M, K)).astype(np.float32)
     y = layer.matmul_host(x)
-    rc, yo = oracle.w4a16_linear(bf16_bits(x), qw, sc, None, g_idx, N, K, 128)
+    rc, yo = oracle.w4a16_linear(bf16_bits(x), qw, sc, qz, g_idx, N, K, 128)
     assert rel_err(y, yo) <= TOL_F32
     # saved again, it round-trips to the same tensors
     path2 = str(tmp_path / "gptq2.safetensors")

@@ -544,3 +544,113 @@ def test_dev_fake_quant_rejects_bad_arguments(lib):
     for scale, bits in ((0.0, 8), (-1.0, 8), (1.0, 1), (1.0, 17)):
         with pytest.raises(Exception):
             lib.dev_fake_quant(x, x, scale, bits)
+
+
+# ------------------------------------------- the bench's exact shapes, fp8 C4
+def _fp8_blocks(M, N, rng, extra=6):
+    blocks = [(0, 0), (M - 64, N - 64), (M - 64, 0), (0, N - 64)]
+    return blocks + [(int(rng.integers(0, M - 64)), int(rng.integers(0, N - 64))) for _ in range(extra)]
+
+
+def test_w8a8_fp8_full_shape_subtiles(lib, oracle):
+    """C4 fp8 at full size through the multi-tile kernel (XCD-aware tile
+    map): sampled 64x64 sub-tiles plus the four corner blocks against the
+    oracle's fp8 product of the same codes."""
+    M, N, K = 2048, 14336, 4096
+    print(f"[gpu] w8a8 fp8 {M}x{N}x{K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(3)
+    a32 = torch.randn((M, K), device=DEV, generator=g)
+    w32 = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    A = torch.empty((M, K), dtype=torch.uint8, device=DEV)
+    W = torch.empty((N, K), dtype=torch.uint8, device=DEV)
+    sA, sW = torch.empty(1, device=DEV), torch.empty(1, device=DEV)
+    lib.dev_quantize_fp8_e4m3_scaled(a32, A, sA)
+    lib.dev_quantize_fp8_e4m3_scaled(w32, W, sW)
+    del a32, w32
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w8a8_fp8(A, sA, W, sW, out)
+    torch.cuda.synchronize()
+    An, Wn, outn = A.cpu().numpy(), W.cpu().numpy(), bf16_to_f32(u16(out))
+    sa, sw = np.float32(sA.item()), np.float32(sW.item())
+    for m0, n0 in _fp8_blocks(M, N, np.random.default_rng(2)):
+        ref = oracle.fp8_gemm(An[m0:m0 + 64], Wn[n0:n0 + 64], sa, sw)
+        assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], ref) <= TOL_BF16, (m0, n0)
+
+
+@pytest.mark.parametrize("M,N,K", [(2148, 7208, 384), (300, 1000, 128), (130, 7205, 256)])
+def test_w8a8_fp8_ragged_multi_tile(lib, oracle, M, N, K):
+    # several tile rows and columns, ragged edge tiles, one- and three-stage
+    # K loops, N not a multiple of 8
+    print(f"[gpu] w8a8 fp8 ragged {M}x{N}x{K}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    rc, A, sa = oracle.quantize_fp8_e4m3_scaled(rng.normal(0, 1, (M, K)).astype(np.float32))
+    rc, W, sw = oracle.quantize_fp8_e4m3_scaled(rng.normal(0, 0.02, (N, K)).astype(np.float32))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w8a8_fp8(to_dev(A), to_dev(np.array([sa], np.float32)), to_dev(W),
+                         to_dev(np.array([sw], np.float32)), out)
+    torch.cuda.synchronize()
+    outn = bf16_to_f32(u16(out))
+    for m0, n0 in _fp8_blocks(M, N, rng):
+        ref = oracle.fp8_gemm(A[m0:m0 + 64], W[n0:n0 + 64], sa, sw)
+        assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], ref) <= TOL_BF16, (m0, n0)
+
+
+def _random_qzeros(rng, N, G):
+    z = rng.integers(0, 16, (N, ((G + 7) // 8) * 8)).astype(np.uint32)
+    z[:, G:] = 0
+    return (z.reshape(N, -1, 8) << (4 * np.arange(8, dtype=np.uint32))).sum(-1).astype(np.uint32)
+
+
+@pytest.mark.parametrize("M,N,K,zeros", [(1, 11008, 4096, False), (8, 11008, 4096, False),
+                                         (1, 11008, 4096, True), (8, 11008, 4096, True),
+                                         (1, 4096, 14336, True), (8, 4096, 14336, True)])
+def test_w4a16_actorder_prepared_bench_shapes(lib, oracle, M, N, K, zeros):
+    """C3 at the bench's shape (N = 11008, three row groups per workgroup in
+    the small-M kernel), and act-order weights that carry zero points (the
+    prepared M = 1 and small-M kernels built with zeros), also at the
+    down-projection width."""
+    print(f"[gpu] w4a16 act-order prepared M={M} N={N} K={K} zeros={zeros}", flush=True)
+    rng = np.random.default_rng(M + N + K + zeros)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 29 + M, g_idx=g_idx)
+    qz = _random_qzeros(rng, N, G) if zeros else None
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), G, qs, perm)
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16_actorder(to_dev(x), qs, to_dev(sc), None if qz is None else to_dev(qz), perm, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, g_idx, N, K, 128)
+    assert rel_err(bf16_to_f32(u16(y)), yo) <= TOL_BF16
+
+
+def test_w4a16_gemv_m16_bench_shape(lib, oracle):
+    # C2 M = 16 exactly as the bench runs it (N = 11008, zero points, bf16 out)
+    M, N, K = 16, 11008, 4096
+    print(f"[gpu] w4a16 gemv M={M} N={N} K={K}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, 128, 116)
+    x = bf16_bits(np.random.default_rng(216).normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, G, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, 128)
+    assert rel_err(bf16_to_f32(u16(y)), yo) <= TOL_BF16
+
+
+@pytest.mark.parametrize("K", [14336, 16384])
+@pytest.mark.parametrize("mean", [3.0, -1.0])
+def test_w8_gemv_activations_far_from_zero_mean(lib, oracle, K, mean):
+    # the unsigned-byte form takes 128 * sum(x) off; with x ~ N(mean, 1) that
+    # term is large, so it must come off per slot, not once per row
+    N = 300
+    print(f"[gpu] w8 gemv mean={mean} K={K}", flush=True)
+    rng = np.random.default_rng(K + int(mean))
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    x = (rng.normal(0, 1, (1, K)) + mean).astype(np.float32)
+    rc, q, s = oracle.quantize_int8_channel(w)
+    y = torch.empty((1, N), device=DEV)
+    lib.qlinear_w8_gemv(to_dev(x), to_dev(q), to_dev(s), y)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w8_linear(x, q, s)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32

@@ -159,3 +159,120 @@ def test_half_even_option_matches_numpy_rint_and_differs_only_at_ties(oracle):
     ties = (np.abs(prod - np.trunc(prod)) == 0.5)
     diff = q_even != q_away
     assert diff.sum() > 0 and np.all(ties[diff])
+
+
+def _nibbles(qw, K):
+    q = np.asarray(qw, np.uint32)
+    return ((q[:, :, None] >> (4 * np.arange(8, dtype=np.uint32))) & 0xF).reshape(q.shape[0], K).astype(np.int64)
+
+
+def _roundf(v):
+    """C roundf (ties away from zero) on float32 values, exact in float64."""
+    v = np.asarray(v, np.float64)
+    return np.sign(v) * np.floor(np.abs(v) + 0.5)
+
+
+def test_w4_awq_ties_and_divide_first(oracle):
+    """The W4 code rule is quantize_int8.c:114-120 with 255 -> 15:
+    roundf(w / s + z) - a division, then an fp32 add, then ties away from
+    zero.  Planted exact ties (w / s + z = k + 0.5 exactly) must give k + 1
+    (rint would give the even neighbour), and values where w * (1/s) and w / s
+    round to different codes must take the division's code."""
+    s = np.float32(3.0 / 1024.0)                      # exact in fp16 and fp32
+    g = 128
+    row = np.zeros(g, np.float32)
+    row[0], row[1] = -5 * s, 10 * s                   # lo, hi: (hi - lo)/15 = s, z = 5
+    ks = np.arange(15)
+    row[2:17] = (ks + 0.5 - 5) * s                    # w/s + z = k + 0.5 exactly
+    # values where multiply-by-reciprocal and divide disagree on the code
+    inv = np.float32(1.0) / s
+    found = []
+    base = ((np.arange(-4, 10) + 0.5) * s).astype(np.float32)
+    for b in base:
+        for d in range(-64, 65):
+            w = np.nextafter(b, np.float32(np.inf if d > 0 else -np.inf)) if d else b
+            for _ in range(abs(d) - 1):
+                w = np.nextafter(w, np.float32(np.inf if d > 0 else -np.inf))
+            q_div = _roundf(np.float32(np.float32(w / s) + np.float32(5)))
+            q_mul = _roundf(np.float32(np.float32(w * inv) + np.float32(5)))
+            if q_div != q_mul and -5 * s < w < 10 * s:
+                found.append((np.float32(w), int(q_div), int(q_mul)))
+    assert found, "no multiply/divide disagreement near the ties"
+    found = found[: g - 17]
+    row[17:17 + len(found)] = [f[0] for f in found]
+    w = np.tile(row, (2, 1))
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, g)
+    assert rc == 0
+    assert sc[0, 0] == np.float16(s).view(np.uint16) and (qz[0, 0] & 0xF) == 5
+    nib = _nibbles(qw, g)[0]
+    assert nib[0] == 0 and nib[1] == 15
+    assert list(nib[2:17]) == list(ks + 1)            # ties away from zero
+    got = nib[17:17 + len(found)]
+    assert list(got) == [f[1] for f in found]         # the division's codes
+    assert all(g_ != f[2] for g_, f in zip(got, found))
+
+
+def test_w8a8_epilogue_against_float64(oracle):
+    """out[m][n] = acc * sA[m] * sW[n]: per-token scales index rows and
+    per-channel scales index columns (M != N, distinct scales, so a swapped
+    or transposed index fails); fp32 rounding only."""
+    rng = np.random.default_rng(8)
+    M, N = 7, 11
+    acc = rng.integers(-2 ** 26, 2 ** 26, (M, N)).astype(np.int32)
+    sA = rng.uniform(1e-3, 2e-2, M).astype(np.float32)
+    sW = rng.uniform(1e-4, 1e-3, N).astype(np.float32)
+    out = oracle.w8a8_epilogue(acc, sA, sW)
+    want = acc.astype(np.float64) * sA[:, None].astype(np.float64) * sW[None, :].astype(np.float64)
+    assert np.all(np.abs(out - want) <= 2.5 * 2.0 ** -24 * np.abs(want))
+    bias = rng.normal(0, 1, N).astype(np.float32)
+    outb = oracle.w8a8_epilogue(acc, sA, sW, bias)
+    wantb = want + bias.astype(np.float64)
+    assert np.all(np.abs(outb - wantb) <= 2.0 ** -22 * (np.abs(want) + np.abs(wantb)))
+    # the full W8A8 reference on dequantised operands (float64) is what the
+    # epilogue of the exact int32 product equals
+    A = rng.integers(-127, 128, (M, 96)).astype(np.int8)
+    W = rng.integers(-127, 128, (N, 96)).astype(np.int8)
+    out2 = oracle.w8a8_epilogue(oracle.i8_gemm_i32(A, W), sA, sW)
+    deq = (A.astype(np.float64) * sA[:, None]) @ (W.astype(np.float64) * sW[:, None]).T
+    assert np.all(np.abs(out2 - deq) <= 2.5 * 2.0 ** -24 * np.abs(deq) + 1e-30)
+
+
+def test_matmul_order_and_layout(oracle):
+    """tensor.c:1820-1823: k-ascending fp32 sum from 0.0f.  [1, 1e8, -1e8]
+    summed in that order is 0 (1 is absorbed by 1e8); reversed it is 1.  The
+    [K,N] and [N,K] forms are transposes of one another and equal float64
+    within fp32 rounding."""
+    a = np.array([[1.0, 1e8, -1e8]], np.float32)
+    ones = np.ones((3, 1), np.float32)
+    assert oracle.matmul_kn(a, ones)[0, 0] == 0.0
+    assert oracle.matmul_nk(a, ones.T)[0, 0] == 0.0
+    assert oracle.matmul_kn(a[:, ::-1].copy(), ones)[0, 0] == 1.0
+    rng = np.random.default_rng(9)
+    x = rng.normal(0, 1, (5, 64)).astype(np.float32)
+    b = rng.normal(0, 1, (64, 7)).astype(np.float32)
+    ykn = oracle.matmul_kn(x, b)
+    ynk = oracle.matmul_nk(x, np.ascontiguousarray(b.T))
+    assert np.array_equal(ykn.view(np.uint32), ynk.view(np.uint32))
+    want = x.astype(np.float64) @ b.astype(np.float64)
+    assert np.abs(ykn - want).max() <= 1e-5 * np.abs(want).max()
+
+
+def test_bias_step(oracle):
+    """quantization.py:451-454: y = x @ W^T + bias.  Zero weights give the
+    bias exactly; otherwise float64 within fp32 rounding."""
+    rng = np.random.default_rng(10)
+    M, N, K, g = 3, 24, 256, 128
+    bias = rng.normal(0, 1, N).astype(np.float32)
+    x = rng.normal(0, 1, (M, K)).astype(np.float32)
+    q0 = np.zeros((N, K), np.int8)
+    rc, y0 = oracle.w8_linear(x, q0, np.ones(N, np.float32), bias)
+    assert rc == 0 and np.array_equal(y0, np.tile(bias, (M, 1)))
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, g)
+    xb = bf16_bits(x)
+    rc, deq = oracle.w4_dequantize(qw, sc, qz, None, N, K, g)
+    rc, y = oracle.w4a16_linear(xb, qw, sc, qz, None, N, K, g, bias)
+    want = bf16_to_f32(xb).astype(np.float64) @ deq.astype(np.float64).T + bias
+    assert np.abs(y - want).max() <= 1e-5 * np.abs(want).max()
+    rc, ynb = oracle.w4a16_linear(xb, qw, sc, qz, None, N, K, g)
+    assert np.array_equal(y, (ynb + bias[None, :]).astype(np.float32))

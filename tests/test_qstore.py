@@ -135,7 +135,7 @@ def test_reads_files_of_the_reference_writer(L, tmp_path):
 
 @needs_lib
 @pytest.mark.parametrize("case", ["short", "huge_header", "not_object", "bad_entry", "past_end",
-                                  "size_mismatch", "trailing"])
+                                  "size_mismatch", "trailing", "byte_overflow"])
 def test_malformed_files_are_rejected_with_a_reason(L, tmp_path, case):
     good = b'{"a":{"dtype":"F32","shape":[2],"data_offsets":[0,8]}}'
     body = {
@@ -146,6 +146,8 @@ def test_malformed_files_are_rejected_with_a_reason(L, tmp_path, case):
         "past_end": struct.pack("<Q", len(good)) + good + b"\0" * 4,
         "size_mismatch": struct.pack("<Q", 54) + b'{"a":{"dtype":"F32","shape":[3],"data_offsets":[0,8]}}' + b"\0" * 8,
         "trailing": struct.pack("<Q", len(good) + 1) + good + b"x" + b"\0" * 8,
+        # 2^62 I32 elements: the byte count wraps to 0, which would match [0, 0]
+        "byte_overflow": struct.pack("<Q", 74) + b'{"q":{"dtype":"I32","shape":[4611686018427387904,1],"data_offsets":[0,0]}}',
     }[case]
     path = str(tmp_path / f"{case}.safetensors")
     open(path, "wb").write(body)
