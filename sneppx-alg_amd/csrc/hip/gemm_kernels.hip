@@ -167,7 +167,7 @@ __device__ __forceinline__ i32x4 lds16(const int8_t* p) { return *reinterpret_ca
 // fp8 (and the 16x16 int8 form): waves in 4 (M) x 2 (N), each 64 x 112 =
 // 4 x 7 MFMA blocks of 16 x 16 (112 accumulators), two waves per SIMD, so one
 // wave's LDS latency hides behind the other's MFMAs.
-template <bool FP8, bool RAW>
+template <bool FP8, bool RAW, bool BIAS>
 __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                                                  const int8_t* __restrict__ W,
                                                  const float* __restrict__ sA,
@@ -238,7 +238,7 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
         for (int j = 0; j < TFN; j++) {
             const int n = n0 + wn * 112 + j * 16 + r16;
             swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
-            bv[j] = bias ? bias[n < N ? n : N - 1] : 0.0f;
+            bv[j] = BIAS ? bias[n < N ? n : N - 1] : 0.0f;
         }
     }
     for (int kt = 0; kt < nk; kt++) {
@@ -302,7 +302,8 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
                 if (RAW)
                     Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
                 else
-                    out[(size_t)m * N + n] = bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j] + bv[j]);
+                    out[(size_t)m * N + n] = BIAS ? bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j] + bv[j])
+                                                  : bf16_out((float)acc[i][j][e] * sa[i][e] * swv[j]);
             }
         }
     }
@@ -478,7 +479,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 constexpr int XCROW = 232;   // u16 per staged output row: 224 + 8 pad
 static_assert(8 * 32 * XCROW * 2 <= 2 * TLDS_STAGE, "output staging fits in the LDS ring");
 
-template <bool FP8, bool RAW>
+template <bool FP8, bool RAW, bool BIAS>
 __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
                                                     const int8_t* __restrict__ W,
                                                     const float* __restrict__ sA,
@@ -541,7 +542,7 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
         for (int j = 0; j < FN; j++) {
             const int n = n0 + j * 32 + r32;
             swv[j] = FP8 ? sW[0] : sW[n < N ? n : N - 1];
-            bv[j] = bias ? bias[n < N ? n : N - 1] : 0.0f;
+            bv[j] = BIAS ? bias[n < N ? n : N - 1] : 0.0f;
         }
     }
     for (int kt = 0; kt < nk; kt++) {
@@ -608,7 +609,8 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
 #pragma unroll
         for (int v = 0; v < 16; v++)
             ct[(8 * (v >> 2) + 4 * h + (v & 3)) * XCROW + j * 32 + r32] =
-                bf16_out((float)acc[j][v] * sa[v] * swv[j] + bv[j]);
+                BIAS ? bf16_out((float)acc[j][v] * sa[v] * swv[j] + bv[j])
+                     : bf16_out((float)acc[j][v] * sa[v] * swv[j]);
     const bool vec = (N & 7) == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
 #pragma unroll
     for (int t = 0; t < 14; t++) {        // 32 rows x 28 pieces = 896 = 14 x 64
@@ -850,7 +852,7 @@ int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* s
     return snx_launch_check("k_gemm_i8p");
 }
 
-template <bool FP8, bool RAW>
+template <bool FP8, bool RAW, bool BIAS>
 int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
                  int32_t* Craw, uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
@@ -860,17 +862,17 @@ int launch_x32(const int8_t* A, const int8_t* W, const float* sA, const float* s
     }
     const size_t lds = 2 * (size_t)TLDS_STAGE;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_gemm_x32<FP8, RAW>);
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_x32<FP8, RAW, BIAS>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_x32<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
+    k_gemm_x32<FP8, RAW, BIAS><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
                                                               K, tiles_m, tiles_n);
     return snx_launch_check("k_gemm_x32");
 }
 
-template <bool FP8, bool RAW>
+template <bool FP8, bool RAW, bool BIAS>
 int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
                  uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
@@ -880,12 +882,12 @@ int launch_tiled(const int8_t* A, const int8_t* W, const float* sA, const float*
     }
     const size_t lds = 2 * (size_t)TLDS_STAGE;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8w<FP8, RAW>);
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8w<FP8, RAW, BIAS>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_8w<FP8, RAW><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
+    k_gemm_8w<FP8, RAW, BIAS><<<tiles_m * tiles_n, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N,
                                                             K, tiles_m, tiles_n);
     return snx_launch_check("k_gemm_8w");
 }
@@ -907,11 +909,12 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
         const bool fits = (uint64_t)M * K < (1ull << 31) && (uint64_t)N * K < (1ull << 31);
         if (c_i32)
             return fits ? launch_i8p<true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
-                        : launch_x32<false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
+                        : launch_x32<false, true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
         if (fits && N % 8 == 0 && (reinterpret_cast<uintptr_t>(out_bf16) & 15) == 0 && (uint64_t)M * N * 2 < BUF_DROP)
             return bias ? launch_i8p<false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
                         : launch_i8p<false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
-        return launch_x32<false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
+        return bias ? launch_x32<false, false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+                    : launch_x32<false, false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
     }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     if (c_i32)
@@ -937,9 +940,15 @@ int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const fl
         snx_set_error("fp8 gemm: K=%zu must be a multiple of 32", K);
         return -1;
     }
-    if (K % TBK == 0 && M >= 128 && N >= 128)
-        return launch_tiled<true, false>(reinterpret_cast<const int8_t*>(A), reinterpret_cast<const int8_t*>(W),
-                                         sA, sW, nullptr, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
+    if (K % TBK == 0 && M >= 128 && N >= 128) {
+        const int8_t* a8 = reinterpret_cast<const int8_t*>(A);
+        const int8_t* w8 = reinterpret_cast<const int8_t*>(W);
+        if (bias)
+            return launch_tiled<true, false, true>(a8, w8, sA, sW, nullptr, out_bf16, bias, (int)M, (int)N,
+                                                   (int)K, S(st));
+        return launch_tiled<true, false, false>(a8, w8, sA, sW, nullptr, out_bf16, bias, (int)M, (int)N,
+                                                (int)K, S(st));
+    }
     dim3 grid((unsigned)((N + 63) / 64), (unsigned)((M + 63) / 64));
     k_fp8_gemm<<<grid, 256, 0, S(st)>>>(A, W, sA, sW, out_bf16, bias, (int)M, (int)N, (int)K);
     return snx_launch_check("k_fp8_gemm");
