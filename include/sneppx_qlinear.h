@@ -108,6 +108,26 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
                          const float* bias, void* y, SNEPPXDtype y_dtype, size_t M, size_t N,
                          size_t K, int group, SNEPPXStream stream);
 
+/* Allocation-free form of SNEPPX_qlinear_w4a16 (no counterpart in the
+ * reference).  For callers that cannot allocate device memory: code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
+ * Same arguments, dispatch and results (bit-identical) as
+ * SNEPPX_qlinear_w4a16, but the scratch the split-K decode and the prefill
+ * GEMM need (fp32 partials, prepared activations) comes from one static
+ * device array of SNEPPX_NOALLOC_SCRATCH_BYTES per GPU, held from the first
+ * call on that GPU until the process ends, instead of a workspace.  A call
+ * that needs more scratch than that returns -1 with the reason (for
+ * example split-K partials K/1024 * M * N * 4 bytes, prefill 2 M K bytes and
+ * more).  Every call on a GPU shares its array: calls that overlap on one GPU
+ * (two streams, two threads) race on it and must be serialised by the
+ * caller.  Nothing in the array needs to start at zero. */
+#define SNEPPX_NOALLOC_SCRATCH_BYTES (32u << 20)
+int SNEPPX_qlinear_w4a16_noalloc(const uint16_t* x, const uint32_t* qweight,
+                                 const uint16_t* scales, const uint32_t* qzeros,
+                                 const int32_t* g_idx, size_t G, const float* bias, void* y,
+                                 SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
+                                 SNEPPXStream stream);
+
 /* C3 fast path, step 1 (once per layer, at load time): GPTQ act-order
  * weights (qweight in column order k, g_idx int32 [K]) -> group-contiguous
  * order.  perm (uint16 [K], device) receives the stable argsort of g_idx and

@@ -115,31 +115,38 @@ int SNEPPX_qlinear_w8_gemv(const float* x, const int8_t* qweight, const float* s
     return snx_k_w8_gemv(x, qweight, scales, y, bias, M, N, K, stream);
 }
 
-int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
-                         const uint32_t* qzeros, const int32_t* g_idx, size_t G,
-                         const float* bias, void* y, SNEPPXDtype y_dtype, size_t M, size_t N,
-                         size_t K, int group, SNEPPXStream stream) {
-    REQUIRE(x && qweight && scales && y, "qlinear_w4a16: NULL pointer");
-    REQUIRE(M && N && K, "qlinear_w4a16: empty shape");
-    REQUIRE(K % 8 == 0, "qlinear_w4a16: K=%zu must be a multiple of 8", K);
+/* Scratch of one W4A16 call: the calling thread's workspace on `stream`, or
+ * for the allocation-free entry point the library's static device array
+ * (NULL, with the error text set, when the call needs more than it holds). */
+static void* w4_scratch(size_t bytes, int noalloc, SNEPPXStream stream) {
+    return noalloc ? snx_noalloc_scratch(bytes, "qlinear_w4a16_noalloc")
+                   : snx_workspace(bytes, 1, stream);
+}
+
+static int w4a16_linear(const char* who, int noalloc, const uint16_t* x, const uint32_t* qweight,
+                        const uint16_t* scales, const uint32_t* qzeros, const int32_t* g_idx,
+                        size_t G, const float* bias, void* y, SNEPPXDtype y_dtype, size_t M,
+                        size_t N, size_t K, int group, SNEPPXStream stream) {
+    REQUIRE(x && qweight && scales && y, "%s: NULL pointer", who);
+    REQUIRE(M && N && K, "%s: empty shape", who);
+    REQUIRE(K % 8 == 0, "%s: K=%zu must be a multiple of 8", who, K);
     REQUIRE(y_dtype == SNEPPX_BFLOAT16 || y_dtype == SNEPPX_FLOAT32,
-            "qlinear_w4a16: y_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32");
+            "%s: y_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32", who);
     int y_f32 = y_dtype == SNEPPX_FLOAT32;
     if (g_idx) {
-        REQUIRE(G > 0, "qlinear_w4a16: G must be > 0 with g_idx");
+        REQUIRE(G > 0, "%s: G must be > 0 with g_idx", who);
     } else {
-        REQUIRE(group > 0 && K % (size_t)group == 0,
-                "qlinear_w4a16: group %d must divide K=%zu", group, K);
+        REQUIRE(group > 0 && K % (size_t)group == 0, "%s: group %d must divide K=%zu", who, group, K);
         G = K / (size_t)group;
     }
     snx_clear_error();
     if (!g_idx && M >= SNX_W4_GEMM_MIN_M && aligned16(x) && aligned16(qweight) &&
         ((uintptr_t)scales & 3u) == 0 && ((uintptr_t)qzeros & 3u) == 0 &&
         snx_w4a16_gemm_ok(M, N, K, group)) {
-        /* prefill GEMM: activations prepared once into a stream-ordered workspace */
+        /* prefill GEMM: activations prepared once into the call's scratch */
         const size_t Mp = snx_w4_prep_rows(M);
         const size_t xp_bytes = (M * K * sizeof(uint16_t) + 255) & ~(size_t)255;
-        char* ws = (char*)snx_workspace(xp_bytes + (K / 128) * Mp * sizeof(float), 1, stream);
+        char* ws = (char*)w4_scratch(xp_bytes + (K / 128) * Mp * sizeof(float), noalloc, stream);
         if (!ws) return -1;
         uint16_t* xp = (uint16_t*)ws;
         float* xs = (float*)(ws + xp_bytes);
@@ -159,7 +166,7 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
         /* 5 <= M <= 16, and 2 <= M <= 4 where the LDS-staged small-M kernel does
          * not apply (large K): split-K decode + ordered reduction of the partials */
         const size_t S = K / (size_t)kspan;
-        float* part = (float*)snx_workspace(S * M * N * sizeof(float), 1, stream);
+        float* part = (float*)w4_scratch(S * M * N * sizeof(float), noalloc, stream);
         if (!part) return -1;
         int rc = snx_k_w4a16_splitk(x, qweight, scales, qzeros, part, M, N, K, group, kspan, stream);
         if (!rc) rc = snx_k_w4a16_reduce(part, y, y_f32, (int)S, M * N, N, bias, stream);
@@ -179,6 +186,23 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
     }
     return snx_k_w4a16_generic(x, qweight, scales, qzeros, g_idx, G, y, bias, y_f32, M, N, K,
                                group, stream);
+}
+
+int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint16_t* scales,
+                         const uint32_t* qzeros, const int32_t* g_idx, size_t G,
+                         const float* bias, void* y, SNEPPXDtype y_dtype, size_t M, size_t N,
+                         size_t K, int group, SNEPPXStream stream) {
+    return w4a16_linear("qlinear_w4a16", 0, x, qweight, scales, qzeros, g_idx, G, bias, y, y_dtype,
+                        M, N, K, group, stream);
+}
+
+int SNEPPX_qlinear_w4a16_noalloc(const uint16_t* x, const uint32_t* qweight,
+                                 const uint16_t* scales, const uint32_t* qzeros,
+                                 const int32_t* g_idx, size_t G, const float* bias, void* y,
+                                 SNEPPXDtype y_dtype, size_t M, size_t N, size_t K, int group,
+                                 SNEPPXStream stream) {
+    return w4a16_linear("qlinear_w4a16_noalloc", 1, x, qweight, scales, qzeros, g_idx, G, bias, y,
+                        y_dtype, M, N, K, group, stream);
 }
 
 /* Stable counting sort of g_idx on the host (one small copy each way). */

@@ -21,6 +21,9 @@ void snx_set_error(const char* fmt, ...);
 void* snx_workspace(size_t bytes, int slot, void* stream);
 /* stream-ordered release of the calling thread's workspaces on `stream` */
 void snx_release_workspaces(void* stream);
+/* the current device's static scratch array (noalloc.hip) when `bytes` fit
+ * in it, else NULL with the error text set (prefixed by `who`) */
+void* snx_noalloc_scratch(size_t bytes, const char* who);
 void snx_clear_error(void);
 int snx_launch_check(const char* kernel);
 

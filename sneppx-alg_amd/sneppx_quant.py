@@ -73,6 +73,8 @@ EXPORTS = {
     "SNEPPX_qlinear_w8_gemv": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w4a16": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, C.c_int, _sz, _sz,
                                        _sz, C.c_int, _vp]),
+    "SNEPPX_qlinear_w4a16_noalloc": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _vp, _vp, C.c_int, _sz, _sz,
+                                               _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_w4_actorder_prepare": (C.c_int, [_vp, _vp, _sz, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz,
                                                 _sz, C.c_int, _vp]),
@@ -340,6 +342,17 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w4a16"](
             _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(bias), _ptr(y),
             ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16")
+
+    def qlinear_w4a16_noalloc(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None,
+                              bias=None):
+        """SNEPPX_qlinear_w4a16_noalloc: as qlinear_w4a16, scratch from the
+        library's static device array instead of a workspace."""
+        M, K = x.shape
+        N = qweight.shape[0]
+        ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_w4a16_noalloc"](
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(bias), _ptr(y),
+            ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16_noalloc")
 
     def qlinear_w4_actorder_prepare(self, qweight, g_idx, G, qweight_sorted, perm, stream=None):
         N, K8 = qweight.shape
