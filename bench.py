@@ -351,8 +351,9 @@ def llama_tokens(seed=5):
 
 def bench_chain(lib, timer, torch, steps, warmup):
     """C5: one Llama-3-8B decoder layer's linears in W4A16 g128 (AWQ-style,
-    random init): QKV 4096->6144, O 4096->4096, gate/up 4096->2x14336,
-    SiLU(gate)*up, down 14336->4096, on T packed tokens.  The O input is a
+    random init): QKV 4096->6144, O 4096->4096, gate/up 4096->2x14336 with
+    SiLU(gate)*up in the GEMM's epilogue, down 14336->4096, on T packed
+    tokens.  The O input is a
     synthetic bf16 tensor (attention is not part of this path); the gate/up
     input is the O output."""
     T, lens = llama_tokens()
@@ -382,19 +383,28 @@ def bench_chain(lib, timer, torch, steps, warmup):
         qw, sc, qz, G = ws[name]
         lib.qlinear_w4a16(inp, qw, sc, qz, None, G, out, 128, stream=st)
 
+    def gate_up_swiglu(inp, out):
+        qw, sc, qz, G = ws["gate_up"]
+        lib.qlinear_w4a16_swiglu(inp, qw, sc, qz, out, 128, stream=st)
+
     def layer():
         lin("qkv", x, y_qkv)
         lin("o", attn, y_o)
-        lin("gate_up", y_o, y_gu)
-        lib.qlinear_silu_mul(y_gu, act, stream=st)
+        gate_up_swiglu(y_o, act)           # gate/up GEMM with SiLU(gate) * up in its epilogue
         lin("down", act, y_d)
 
     total, _, _ = timer.run([layer], steps, warmup)
     per = {}
-    for name, inp, out in (("qkv", x, y_qkv), ("o", attn, y_o), ("gate_up", y_o, y_gu), ("down", act, y_d)):
-        t, _, _ = timer.run([lambda n=name, i=inp, o=out: lin(n, i, o)], steps, 2)
-        N, K = shapes[name]
+    for name, fn in (("qkv", lambda: lin("qkv", x, y_qkv)), ("o", lambda: lin("o", attn, y_o)),
+                     ("gate_up+swiglu", lambda: gate_up_swiglu(y_o, act)),
+                     ("down", lambda: lin("down", act, y_d))):
+        t, _, _ = timer.run([fn], steps, 2)
+        N, K = shapes[name.split("+")[0]]
         per[name] = {"us": round(t / steps * 1e3, 1), "tflops": round(2 * T * N * K / (t / steps) / 1e9, 1)}
+    # the unfused form for comparison: the [T][2F] projection in bf16, then the SwiGLU pass
+    t, _, _ = timer.run([lambda: (lin("gate_up", y_o, y_gu), lib.qlinear_silu_mul(y_gu, act, stream=st))],
+                        steps, 2)
+    per["gate_up then silu_mul (unfused)"] = {"us": round(t / steps * 1e3, 1)}
     flops = 2 * T * sum(N * K for N, K in shapes.values())
     host = {"x": _u16(x[:2 * CPU_ROWS]), "attn": _u16(attn[:2 * CPU_ROWS]), "shapes": shapes,
             "w": {name: (_u32(qw), _u16(sc), _u32(qz)) for name, (qw, sc, qz, G) in ws.items()}}

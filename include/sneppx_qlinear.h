@@ -156,6 +156,22 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
 int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
                             SNEPPXStream stream);
 
+/* C5 gate/up projection with the SwiGLU step fused (no reference
+ * counterpart for the fused form; the activation is the SWIGLU rule of
+ * kernel/activations/gated_activations.c:33-52, act = g / (1 + exp(-g)),
+ * out = act * u).  qweight / scales / qzeros hold the stacked gate/up
+ * projection [2F][K] in the W4 layout, gate rows first; bias is fp32 [2F]
+ * or NULL.  out bf16 [M][F] = bf16(silu(g) * u) with g = x . Wg^T + bias[n]
+ * and u = x . Wu^T + bias[F + n] kept in fp32 (no bf16 round trip of the
+ * [M][2F] projection).  M >= 256 runs the prefill GEMM with the SwiGLU in
+ * its epilogue; fewer rows run the decode linear into fp32 scratch, then
+ * the same rule.  The exponential and reciprocal use the hardware's fast
+ * approximations (about 1 ulp, below the bf16 rounding).  F % 8 == 0. */
+int SNEPPX_qlinear_w4a16_swiglu(const uint16_t* x, const uint32_t* qweight,
+                                const uint16_t* scales, const uint32_t* qzeros, const float* bias,
+                                uint16_t* out, size_t M, size_t F, size_t K, int group,
+                                SNEPPXStream stream);
+
 /* SNEPPX_qlinear_silu_mul fused with the per-token int8 quantizer the W8A8
  * down projection needs (no reference counterpart; the rule is
  * SNEPPX_quantize_int8_channel, quantize_int8.c:157-177, applied to the bf16

@@ -102,6 +102,12 @@ SNX_HD float f16_to_f32(uint16_t h) {
     return u2f(sign | (e + 112u) << 23 | m << 13);
 }
 
+// Device kernels: the same value with one v_cvt_f32_f16 (exact for every
+// fp16, subnormals included: gfx9 keeps fp16 denormals).
+__device__ __forceinline__ float f16_dev(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
 // Stored W4 scale: fp16, kept positive-finite (underflow -> 2^-24, overflow -> 65504).
 SNX_HD uint16_t w4_scale_f16(float s) {
     uint16_t h = f32_to_f16(s);

@@ -252,7 +252,7 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv(const uint16_t* __restrict__
             if (sc + c >= steps) break;
             const int kbase = (s0 + sc + c) * 128;
             const int g = kbase / group;
-            const float sf = f16_to_f32(scales[(size_t)n * G + g]);
+            const float sf = f16_dev(scales[(size_t)n * G + g]);
             uint32_t z = 8;
             if (ZEROS) z = (qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u;
             const uint32_t negc = (0xC300u | z) * 0x00010001u;   // bf16 -(128 + z), twice
@@ -680,7 +680,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         for (int t = 0; t < T; t++) {
             const int g = 16 * t + (lane >> 2);                 // group of chunk 64 t + lane
             const uint32_t sw = ssc[wr * (G / 2) + (g >> 1)];
-            const float s = f16_to_f32((uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
+            const float s = f16_dev((uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
             const uint32_t z = ZEROS ? (szr[wr * ZPR + (g >> 3)] >> (4 * (g & 7))) & 15u : 8u;
             sc[r][t] = s;
             corr[r] = fmaf(s * (float)(128u + z), X[t], corr[r]);
@@ -1168,7 +1168,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[c][e], __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
             }
             const int gq = wave * NC + c;
-            const float s = f16_to_f32((uint16_t)(sc[c >> 1] >> (16 * (c & 1))));
+            const float s = f16_dev((uint16_t)(sc[c >> 1] >> (16 * (c & 1))));
             const uint32_t zword = (NZ == 2 && (gq >> 3) != ((wave * NC) >> 3)) ? zw[NZ - 1] : zw[0];
             const uint32_t z = ZEROS ? (zword >> (4 * (gq & 7))) & 15u : 8u;
             const float cs = s * (float)(128u + z);
@@ -1268,7 +1268,7 @@ __global__ void __launch_bounds__(256) k_w4a16_generic(const uint16_t* __restric
                 g = g < 0 ? 0 : (g >= G ? G - 1 : g);   // out-of-range g_idx stays in bounds
                 const int z = qz ? (int)((qz[(size_t)n * zw + (g >> 3)] >> (4 * (g & 7))) & 15u) : 8;
                 const float deq = (float)((int)((w >> (4 * t)) & 15u) - z) *
-                                  f16_to_f32(scales[(size_t)n * G + g]);
+                                  f16_dev(scales[(size_t)n * G + g]);
                 acc += bf16_to_f32(x[(size_t)m * K + k]) * deq;
             }
         }

@@ -110,7 +110,20 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // each weight column in lanes with h = l / 32, so a lane's eight words for the
 // step are 32 contiguous bytes; the prep pass stores the activations to match
 // (chunk 2 s + h of a prepared row = original columns of word 8 h + s).
-template <bool ZEROS, bool YF32, int WN>
+// SiLU(g) * u as the fused SwiGLU epilogue computes it: the exponential and
+// the reciprocal on the hardware's fast approximations (about 1 ulp each,
+// far below the bf16 rounding of the result).  Large negative g gives
+// exp = inf, rcp = 0 and a zero product; NaN propagates.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+    return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
+// SWIGLU: the weights are a stacked [2F][K] gate/up projection and the output
+// is [M][F] = bf16(silu(gate) * up) (N = F).  Tile column c < 128 is gate
+// column n0 + c, column c >= 128 the up column F + n0 + c - 128 of the same
+// output column, so waves 0-3 hold gate values and waves 4-7 the matching up
+// values; the epilogue pairs them through LDS.
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU>
 __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
                                                     const float* __restrict__ xs,
                                                     const uint32_t* __restrict__ qw,
@@ -135,7 +148,13 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     const int b = blockIdx.x, nb = gridDim.x;
     const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
     const int tm = tile % tiles_m, tn = tile / tiles_m;
-    const int m0 = tm * GBM, n0 = tn * GBN;
+    const int m0 = tm * GBM, n0 = tn * (SWIGLU ? GBN / 2 : GBN);
+    // weight row of tile column c (clamped into the matrix)
+    auto wcol = [&](int c) -> int {
+        if (!SWIGLU) return n0 + c < N ? n0 + c : N - 1;
+        const int o = n0 + (c & (GBN / 2 - 1)) < N ? n0 + (c & (GBN / 2 - 1)) : N - 1;
+        return c < GBN / 2 ? o : N + o;
+    };
 
     // direct-load sources (byte offsets; operands < 4 GiB).  A: wave w,
     // instruction i fills 1 KB block 8 i + w = tile rows 4 blk .. 4 blk + 3,
@@ -155,13 +174,12 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int row = (8 * i + wave) * 16 + (lane >> 2);
-        const int gn = n0 + row < N ? n0 + row : N - 1;
+        const int gn = wcol(row);
         gw[i] = (uint32_t)gn * wrowb + (uint32_t)((lane & 3) ^ bsw(row)) * 16u;
     }
     // scales (waves 0-3) or zero words (waves 4-7) of tile column 64 (w&3) + lane;
     // without zero points waves 4-7 repeat the scale load (same bytes, same slot)
-    const int scol = n0 + 64 * (wave & 3) + lane;
-    const int sn = scol < N ? scol : N - 1;
+    const int sn = wcol(64 * (wave & 3) + lane);
     const bool zload = ZEROS && wave >= 4;
     const int zw = (G + 7) >> 3;
     // buffer resources: buffer_load ... lds is counted by vmcnt alone, so
@@ -308,6 +326,43 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     }
     __builtin_amdgcn_s_waitcnt(0x0070);   // the ring's last (unused) loads drain before exit
 
+    if constexpr (SWIGLU) {
+        static_assert(WN == 8 && FN == 1 && RW == GBM, "SwiGLU pairs wave w with wave w + 4");
+        // every wave is done with the ring: reuse it for the fp32 gate and up
+        // tiles, [256 tile columns][GBM rows + 1] (the pad spreads the banks)
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+        constexpr int XS = GBM + 1;
+        float* ex = reinterpret_cast<float*>(lds);
+        const int c = wn * CW + r32;                            // tile column 0..255
+        const float bv = bias ? bias[wcol(c)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < QM; i++)
+#pragma unroll
+            for (int u = 0; u < 2; u++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    ex[c * XS + 32 * (2 * i + u) + 8 * (v >> 2) + 4 * h + (v & 3)] = yq[i][0][16 * u + v] + bv;
+        __builtin_amdgcn_s_waitcnt(0xc07f);
+        __builtin_amdgcn_s_barrier();
+        // wave w: output rows 16 w .. 16 w + 15, two columns per lane
+        const int oc = 2 * (lane & 63);                         // output column pair 0..126
+        const int n = n0 + oc;
+#pragma unroll 4
+        for (int r = 0; r < 16; r++) {
+            const int row = 16 * wave + r, m = m0 + row;
+            const float g0 = ex[oc * XS + row], g1 = ex[(oc + 1) * XS + row];
+            const float u0 = ex[(oc + GBN / 2) * XS + row], u1 = ex[(oc + 1 + GBN / 2) * XS + row];
+            const uint32_t packed = (uint32_t)bf16_out(silu_mul_fast(g0, u0)) |
+                                    (uint32_t)bf16_out(silu_mul_fast(g1, u1)) << 16;
+            if (m < M && n + 1 < N)
+                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(y) + (size_t)m * N + n) = packed;
+            else if (m < M && n < N)
+                reinterpret_cast<uint16_t*>(y)[(size_t)m * N + n] = (uint16_t)packed;
+        }
+        return;
+    }
+
     // value 16 u + v of pair (i, j), lane l: block (2 i + u, j), row
     // 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32
 #pragma unroll
@@ -332,20 +387,21 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     }
 }
 
-template <bool ZEROS, bool YF32, int WN>
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU>
 int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                    const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
                    int N, int K, int group, int Mp, hipStream_t st) {
-    const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + GBN - 1) / GBN;
+    const int tn_cols = SWIGLU ? GBN / 2 : GBN;
+    const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + tn_cols - 1) / tn_cols;
     const size_t lds = (size_t)GSTAGES * GRING;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN>);
+    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
     const int gshift = __builtin_ctz((unsigned)group);
-    k_w4a16_gemm<ZEROS, YF32, WN><<<tiles_m * tiles_n, 512, lds, st>>>(
+    k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU><<<tiles_m * tiles_n, 512, lds, st>>>(
         xp, xs, qw, scales, qz, y, bias, M, N, K, K / group, gshift, Mp, tiles_m);
     return snx_launch_check("k_w4a16_gemm");
 }
@@ -375,6 +431,25 @@ __global__ void __launch_bounds__(256) k_silu_mul(const uint16_t* __restrict__ g
     u32x4 o;
 #pragma unroll
     for (int e = 0; e < 4; e++) o[e] = silu_mul_pair(gv[e], uv[e]);
+    *reinterpret_cast<u32x4*>(out + t * (size_t)F + f) = o;
+}
+
+// fp32 gate/up [T][2F] -> bf16(silu(g) * u) [T][F], the rule of the fused
+// SwiGLU epilogue (silu_mul_fast); one thread per 8 columns.
+__global__ void __launch_bounds__(256) k_silu_mul_f32(const float* __restrict__ gu,
+                                                      uint16_t* __restrict__ out, int F, size_t items) {
+    const size_t it = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (it >= items) return;
+    const int f8n = F >> 3;
+    const size_t t = it / (size_t)f8n;
+    const int f = (int)(it - t * (size_t)f8n) * 8;
+    const float* g = gu + t * (size_t)(2 * F) + f;
+    const float* u = g + F;
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        o[e] = (uint32_t)bf16_out(silu_mul_fast(g[2 * e], u[2 * e])) |
+               (uint32_t)bf16_out(silu_mul_fast(g[2 * e + 1], u[2 * e + 1])) << 16;
     *reinterpret_cast<u32x4*>(out + t * (size_t)F + f) = o;
 }
 
@@ -442,6 +517,12 @@ __global__ void __launch_bounds__(256) k_silu_mul_quant_int8(const uint16_t* __r
 
 extern "C" {
 
+int snx_k_silu_mul_f32(const float* gu, uint16_t* out, size_t T, size_t F, void* st) {
+    const size_t items = T * (F / 8);
+    k_silu_mul_f32<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(gu, out, (int)F, items);
+    return snx_launch_check("k_silu_mul_f32");
+}
+
 int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* st) {
     const size_t items = T * (F / 8);
     k_silu_mul<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(gu, out, (int)F, items);
@@ -480,11 +561,21 @@ int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
     const int m = (int)M, n = (int)N, k = (int)K, mp = (int)Mp;
     if (qzeros) {
-        if (y_f32) return launch_w4_gemm<true, true, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
-        return launch_w4_gemm<true, false, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+        if (y_f32) return launch_w4_gemm<true, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+        return launch_w4_gemm<true, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
     }
-    if (y_f32) return launch_w4_gemm<false, true, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
-    return launch_w4_gemm<false, false, W4_WN>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+    if (y_f32) return launch_w4_gemm<false, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+    return launch_w4_gemm<false, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+}
+
+int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                            const uint16_t* scales, const uint32_t* qzeros, uint16_t* out,
+                            const float* bias, size_t M, size_t F, size_t K, int group, size_t Mp,
+                            void* st) {
+    const int m = (int)M, f = (int)F, k = (int)K, mp = (int)Mp;
+    if (qzeros)
+        return launch_w4_gemm<true, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, S(st));
+    return launch_w4_gemm<false, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, S(st));
 }
 
 }  // extern "C"

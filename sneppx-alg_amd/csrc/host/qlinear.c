@@ -274,6 +274,41 @@ int SNEPPX_qlinear_w4a16_actorder(const uint16_t* x, const uint32_t* qweight_sor
     return rc;
 }
 
+int SNEPPX_qlinear_w4a16_swiglu(const uint16_t* x, const uint32_t* qweight,
+                                const uint16_t* scales, const uint32_t* qzeros, const float* bias,
+                                uint16_t* out, size_t M, size_t F, size_t K, int group,
+                                SNEPPXStream stream) {
+    REQUIRE(x && qweight && scales && out, "qlinear_w4a16_swiglu: NULL pointer");
+    REQUIRE(M && F && K, "qlinear_w4a16_swiglu: empty shape");
+    REQUIRE(F % 8 == 0 && K % 8 == 0, "qlinear_w4a16_swiglu: F=%zu and K=%zu must be multiples of 8",
+            F, K);
+    REQUIRE(group > 0 && K % (size_t)group == 0, "qlinear_w4a16_swiglu: group %d must divide K=%zu",
+            group, K);
+    REQUIRE(aligned16(out), "qlinear_w4a16_swiglu: out must be 16-byte aligned");
+    snx_clear_error();
+    if (M >= SNX_W4_GEMM_MIN_M && aligned16(x) && aligned16(qweight) &&
+        ((uintptr_t)scales & 3u) == 0 && ((uintptr_t)qzeros & 3u) == 0 &&
+        snx_w4a16_gemm_ok(M, 2 * F, K, group)) {
+        const size_t Mp = snx_w4_prep_rows(M);
+        const size_t xp_bytes = (M * K * sizeof(uint16_t) + 255) & ~(size_t)255;
+        char* ws = (char*)snx_workspace(xp_bytes + (K / 128) * Mp * sizeof(float), 1, stream);
+        if (!ws) return -1;
+        uint16_t* xp = (uint16_t*)ws;
+        float* xs = (float*)(ws + xp_bytes);
+        int rc = snx_k_w4_prep_x(x, xp, xs, M, K, Mp, stream);
+        if (!rc) rc = snx_k_w4a16_gemm_swiglu(xp, xs, qweight, scales, qzeros, out, bias, M, F, K,
+                                              group, Mp, stream);
+        return rc;
+    }
+    /* decode rows: the [M][2F] projection in fp32 scratch, then the same rule */
+    float* gu = (float*)snx_workspace(M * 2 * F * sizeof(float), 0, stream);
+    if (!gu) return -1;
+    int rc = SNEPPX_qlinear_w4a16(x, qweight, scales, qzeros, NULL, 0, bias, gu, SNEPPX_FLOAT32, M,
+                                  2 * F, K, group, stream);
+    if (!rc) rc = snx_k_silu_mul_f32(gu, out, M, F, stream);
+    return rc;
+}
+
 int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
                             SNEPPXStream stream) {
     REQUIRE(gate_up && out, "qlinear_silu_mul: NULL pointer");

@@ -165,6 +165,14 @@ int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
 int snx_k_silu_mul_quant_int8(const uint16_t* gu, int8_t* q, float* scales, size_t T, size_t F,
                               void* stream);
 int snx_k_silu_mul(const uint16_t* gu, uint16_t* out, size_t T, size_t F, void* stream);
+/* the fused SwiGLU rule on fp32 gate/up rows [T][2F] -> bf16 [T][F] */
+int snx_k_silu_mul_f32(const float* gu, uint16_t* out, size_t T, size_t F, void* stream);
+/* the prefill GEMM with the SwiGLU epilogue: qw is the stacked [2F][K]
+ * gate/up projection, out bf16 [M][F], bias fp32 [2F] or NULL */
+int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                            const uint16_t* scales, const uint32_t* qzeros, uint16_t* out,
+                            const float* bias, size_t M, size_t F, size_t K, int group, size_t Mp,
+                            void* stream);
 
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
                   int32_t* c_i32, uint16_t* out_bf16, const float* bias, size_t M, size_t N,

@@ -79,6 +79,7 @@ EXPORTS = {
     "SNEPPX_qlinear_w4a16_actorder": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz,
                                                 _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w4a16_swiglu": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul_quant_int8": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_int8_channel_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -368,6 +369,14 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w4a16_actorder"](
             _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(bias), _ptr(y),
             ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
+
+    def qlinear_w4a16_swiglu(self, x, qweight, scales, qzeros, out, group, stream=None, bias=None):
+        """out [M][F] = bf16(silu(x . Wg^T) * (x . Wu^T)), qweight the stacked [2F][K/8]."""
+        M, K = x.shape
+        F = out.shape[1]
+        self.check(self.fn["SNEPPX_qlinear_w4a16_swiglu"](
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out), M, F, K, group,
+            self._stream(stream)), "qlinear_w4a16_swiglu")
 
     def qlinear_silu_mul(self, gate_up, out, stream=None):
         T, F2 = gate_up.shape

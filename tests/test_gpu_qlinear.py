@@ -654,3 +654,59 @@ def test_w8_gemv_activations_far_from_zero_mean(lib, oracle, K, mean):
     torch.cuda.synchronize()
     rc, yo = oracle.w8_linear(x, q, s)
     assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
+# ------------------------------------------- gate/up projection + SwiGLU fused
+@pytest.mark.parametrize("M,F,K,sym,bias", [
+    (300, 1000, 1024, False, False),    # fused GEMM epilogue, F not a multiple of 128
+    (256, 512, 4096, True, True),       # one M tile, symmetric, bias
+    (600, 14336, 4096, False, False),   # the Llama MLP width (sampled rows)
+    (4, 1000, 4096, False, True),       # decode rows: fp32 projection, then the same rule
+    (1, 512, 2048, True, False),
+])
+def test_w4a16_swiglu(lib, oracle, M, F, K, sym, bias):
+    """out = bf16(silu(g) * u), g / u the gate / up halves of the stacked
+    [2F][K] projection (gated_activations.c:33-52 SWIGLU on the fp32 linear),
+    against the oracle linear and a float64 SiLU."""
+    print(f"[gpu] w4a16 swiglu M={M} F={F} K={K} sym={sym} bias={bias}", flush=True)
+    rng = np.random.default_rng(M + F)
+    qw, sc, qz, G = _w4_case(oracle, 2 * F, K, 128, M + K, sym=sym)
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    b = rng.normal(0, 0.5, 2 * F).astype(np.float32) if bias else None
+    out = torch.empty((M, F), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16_swiglu(to_dev(x), to_dev(qw), to_dev(sc), None if qz is None else to_dev(qz), out, 128,
+                             bias=None if b is None else to_dev(b))
+    torch.cuda.synchronize()
+    rows = np.arange(M) if M * F <= 300 * 1000 else np.array(sorted({0, 1, 127, 128, M // 2, M - 2, M - 1}))
+    rc, gu = oracle.w4a16_linear(x[rows], qw, sc, qz, None, 2 * F, K, 128, bias=b)
+    g, u = gu[:, :F].astype(np.float64), gu[:, F:].astype(np.float64)
+    want = g / (1.0 + np.exp(-g)) * u
+    got = bf16_to_f32(u16(out)[rows]).astype(np.float64)
+    assert rel_err(got, want) <= TOL_BF16
+    # elementwise: one bf16 rounding plus the fp32 linear's own error
+    assert np.all(np.abs(got - want) <= 2.0 ** -8 * np.abs(want) + 1e-4 * np.abs(want).max())
+
+
+@pytest.mark.parametrize("M,K,group", [(1, 4096, 128), (4, 4096, 128), (2, 1024, 256), (8, 14336, 128),
+                                       (3, 96, 32)])
+def test_w4a16_subnormal_fp16_scales(lib, oracle, M, K, group):
+    """Rows of tiny weights get fp16-subnormal group scales (range/15 below
+    2^-14); every decode kernel must decode them exactly (the hardware
+    fp16 -> fp32 conversion keeps fp16 denormals).  The tiny rows are checked
+    as a group, normwise among themselves, so the large rows cannot hide
+    them; a scale flushed to zero would give a relative error of 1."""
+    N = 48
+    print(f"[gpu] w4a16 subnormal scales M={M} K={K} g={group}", flush=True)
+    rng = np.random.default_rng(K + M)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w[::3] *= 1e-4                                          # scales ~ 1e-5: subnormal fp16
+    rc, qw, sc, qz = oracle.w4_awq_quantize(w, group)
+    assert ((sc[::3] & 0x7C00) == 0).mean() > 0.9            # mostly subnormal scales
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, K // group, y, group)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group)
+    got = y.cpu().numpy()
+    assert np.abs(yo[:, ::3]).max() < 1e-3 * np.abs(yo[:, 1::3]).max()
+    assert rel_err(got[:, ::3], yo[:, ::3]) <= TOL_F32
