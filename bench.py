@@ -30,6 +30,9 @@ INT8_PEAK_TOPS = 5033.2        # dense int8 MFMA (256 CU x 8192 op/clk x 2.4 GHz
 FP8_PEAK_TOPS = 5033.2         # dense fp8 MFMA
 BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
 FP4_PEAK_TFLOPS = 10066.3      # dense fp4 MFMA (MXFP4)
+FP6_PEAK_TFLOPS = 10066.3      # dense fp6 MFMA (MXFP6)
+MX_BENCH = {"mxfp4_e2m1": FP4_PEAK_TFLOPS, "mxfp8_e4m3": FP8_PEAK_TOPS, "mxfp8_e5m2": FP8_PEAK_TOPS,
+            "mxfp6_e3m2": FP6_PEAK_TFLOPS, "mxfp6_e2m3": FP6_PEAK_TFLOPS}
 SNEPPX_BFLOAT16 = 3            # SNEPPXDtype of include/sneppx_qlinear.h
 METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
 
@@ -290,21 +293,31 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
             "tops_kernel": ops / mean_launch / 1e9, "host": host}
 
 
-def bench_mxfp4(lib, timer, torch, M, N, K, steps, warmup):
-    """MXFP4 x MXFP4 GEMM (f4 row): operands quantized on the GPU with the
-    reference's MX rule, the product on the scaled fp4 matrix cores."""
+def bench_mx(lib, timer, torch, M, N, K, steps, warmup, fmt="mxfp4_e2m1", mfma_form=False):
+    """MX x MX GEMM (f4 row): operands quantized on the GPU with the
+    reference's MX rule, the product on the scaled f8f6f4 matrix cores.
+    mfma_form: FP8 operands converted to the matrix cores' encoding before
+    the timed region (weights kept converted); otherwise every call converts
+    both operands."""
     g = torch.Generator(device="cuda").manual_seed(19)
     a = torch.randn((M, K), device="cuda", generator=g)
     w = torch.randn((N, K), device="cuda", generator=g) * 0.02
-    pa, sa = lib.dev_quantize_mx(a, "mxfp4_e2m1")
-    pw, sw = lib.dev_quantize_mx(w, "mxfp4_e2m1")
+    pa, sa = lib.dev_quantize_mx(a, fmt)
+    pw, sw = lib.dev_quantize_mx(w, fmt)
     del a, w
+    if mfma_form:
+        pa, sa, _ = lib.mx_to_mfma(pa, sa, M, K, fmt)
+        pw, sw, _ = lib.mx_to_mfma(pw, sw, N, K, fmt)
     out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
     st = timer.stream
-    total, _, _ = timer.run([lambda: lib.qlinear_mxfp4_gemm(pa, sa, pw, sw, out, M, N, K, stream=st)],
-                            steps, warmup)
+    if fmt == "mxfp4_e2m1" and not mfma_form:
+        call = lambda: lib.qlinear_mxfp4_gemm(pa, sa, pw, sw, out, M, N, K, stream=st)
+    else:
+        call = lambda: lib.qlinear_mx_gemm(pa, sa, pw, sw, fmt, out, M, N, K, stream=st, mfma_form=mfma_form)
+    total, mean_launch, _ = timer.run([call], steps, warmup)
     flops = 2 * M * N * K
-    return {"ms_per_step": total / steps, "tflops": flops / (total / steps) / 1e9}
+    return {"ms_per_step": total / steps, "tflops": flops / (total / steps) / 1e9,
+            "tflops_kernel": flops / mean_launch / 1e9}
 
 
 def bench_vendor_w8a8(torch, M, N, K, steps, warmup):
@@ -576,8 +589,9 @@ def run_only(args, lib, timer, torch, N, K, group):
         t, _, _ = timer.run([lambda: lib.qlinear_w4a16(x, qw, sc, qz, None, K2 // 128, y, 128, stream=st)], steps, 2)
         print(f"gemm-w4 T={T} N={N2} K={K2}: {t / steps * 1e3:.1f} us, {2 * T * N2 * K2 / (t / steps) / 1e9:.0f} TFLOP/s")
     elif args.only == "mx":
-        r = bench_mxfp4(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup)
-        print(f"mxfp4 gemm: {r['ms_per_step'] * 1e3:.1f} us, {r['tflops']:.0f} TFLOP/s")
+        for fmt in MX_BENCH:
+            r = bench_mx(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fmt)
+            print(f"{fmt} gemm: {r['ms_per_step'] * 1e3:.1f} us, {r['tflops']:.0f} TFLOP/s")
     elif args.only == "chain":
         r = bench_chain(lib, timer, torch, steps, 2)
         print(f"chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s {r['per_linear']}")
@@ -673,11 +687,17 @@ def main():
             cpu_jobs.append((extra[-1], "fp8" if fp8 else "i8", r["host"]))
         torch.cuda.synchronize()
         extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, 50, 30))
-        r = bench_mxfp4(lib, timer, torch, 2048, 14336, 4096, 50, 30)
-        extra.append({"workload": "MXFP4 x MXFP4 GEMM M=2048 N=14336 K=4096 (reference MX encoding, bf16 out)",
-                      "value": round(r["tflops"], 1), "unit": "TFLOP/s",
-                      "frac_of_peak": round(r["tflops"] / FP4_PEAK_TFLOPS, 4),
-                      "ms_per_step": round(r["ms_per_step"], 4)})
+        for fmt, peak in MX_BENCH.items():
+            for kept in ((False, True) if fmt.startswith("mxfp8") else (False,)):
+                r = bench_mx(lib, timer, torch, 2048, 14336, 4096, 50, 30, fmt, mfma_form=kept)
+                how = ("operands kept in matrix-core form" if kept else
+                       "both operands converted every call" if fmt.startswith("mxfp8") else
+                       "reference MX encoding")
+                extra.append({"workload": f"{fmt.upper()} GEMM M=2048 N=14336 K=4096 ({how}, bf16 out)",
+                              "value": round(r["tflops"], 1), "unit": "TFLOP/s",
+                              "frac_of_peak": round(r["tflops"] / peak, 4),
+                              "ms_per_step": round(r["ms_per_step"], 4)})
+                print(f"[bench] {extra[-1]['workload']}: {r['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
 
     cpu = None
     if not args.no_cpu:

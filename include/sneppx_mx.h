@@ -79,6 +79,40 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
                               const int8_t* sW, void* out, SNEPPXDtype out_dtype, size_t M,
                               size_t N, size_t K, SNEPPXStream stream);
 
+/* The same linear for every block-32 MX format (no reference counterpart):
+ * A [M][K] and W [N][K] both in `fmt` (MXFP8 E4M3 / E5M2, MXFP6 E3M2 / E2M3,
+ * MXFP4), as SNEPPX_dev_quantize_mx writes them with the default block;
+ * out bf16 or fp32 [M][N], fp32 accumulation on the scaled f8f6f4 matrix
+ * cores (the block exponents go in as their E8M0 scales).  FP6 and FP4 codes
+ * are the matrix cores' own.  The reference's FP8 codes with an all-ones
+ * exponent field (E4M3 0x7F = 480, E5M2 65536 .. 114688) are not, so MXFP8
+ * operands first pass through SNEPPX_mx_to_mfma into the calling thread's
+ * workspace (one read and write of A and W per call).  MXFP8/6: K % 128 == 0,
+ * exponents 4-byte aligned; MXFP4 as SNEPPX_qlinear_mxfp4_gemm. */
+int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                           SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype, size_t M,
+                           size_t N, size_t K, SNEPPXStream stream);
+
+/* Reference MX codes of a [rows][cols] block-32 tensor -> codes and
+ * exponents the matrix cores decode to the same values (no reference
+ * counterpart).  MXFP8: every block holding an all-ones-exponent code is
+ * re-encoded one binade lower with its exponent + 1 -- exact, except that
+ * elements worth an odd number of the smallest subnormal at the new exponent
+ * round half to even (counted into *rounded, a device counter, when given);
+ * a block already at exponent 127 is left as it is.  Other formats are copied.
+ * For weights converted once and kept: SNEPPX_qlinear_mx_gemm_mfma then skips
+ * the per-call conversion.  cols % 32 == 0. */
+int SNEPPX_mx_to_mfma(const uint8_t* packed, const int8_t* scales, uint8_t* out_packed,
+                      int8_t* out_scales, size_t rows, size_t cols, SNEPPXMXFormat fmt,
+                      unsigned int* rounded, SNEPPXStream stream);
+
+/* SNEPPX_qlinear_mx_gemm on operands already in matrix-core form
+ * (SNEPPX_mx_to_mfma output, or FP6 / FP4 tensors as quantized). */
+int SNEPPX_qlinear_mx_gemm_mfma(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                                const int8_t* sW, SNEPPXMXFormat fmt, void* out,
+                                SNEPPXDtype out_dtype, size_t M, size_t N, size_t K,
+                                SNEPPXStream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -180,3 +180,61 @@ def dequantize(packed, scales, shape, fmt, block_size=None):
     vals = decode(codes, sp).reshape(rows, nb, bs)
     s = np.asarray(scales, np.float32).reshape(rows, nb).astype(np.float64)
     return (vals * 2.0 ** s[..., None]).reshape(rows, nb * bs)[:, :cols]
+
+
+# ------------------------------------------------------------------------
+# Matrix-core form of the reference's codes (build-defined, no reference
+# counterpart).  The gfx950 scaled MFMA decodes FP8 operands as the OCP
+# formats, in which the all-ones exponent field is not finite; the
+# reference's MXFP8 decode (mx_formats.py:75-96) makes it finite.  FP6 / FP4
+# agree with OCP everywhere.
+
+def ocp_decode(codes, fmt):
+    """Value of each code as the OCP format the matrix cores use: E4M3FN
+    (0x7F / 0xFF NaN, every other code as the reference decodes it), E5M2
+    (exponent field 31: +-inf for mantissa 0, else NaN); FP6 / FP4 as the
+    reference.  Independent of the reference decoder above: the OCP MX spec's
+    formats written out directly."""
+    sp = SPECS[fmt]
+    c = np.asarray(codes, np.int64)
+    sign = np.where((c >> (sp.bits - 1)) & 1, -1.0, 1.0)
+    e = (c >> sp.mant_bits) & ((1 << sp.exp_bits) - 1)
+    m = c & ((1 << sp.mant_bits) - 1)
+    sub = m * 2.0 ** (1 - sp.bias - sp.mant_bits)
+    norm = (2 ** sp.mant_bits + m) * 2.0 ** (e.astype(np.float64) - sp.bias - sp.mant_bits)
+    val = sign * np.where(e == 0, sub, norm)
+    top = (1 << sp.exp_bits) - 1
+    if fmt == "mxfp8_e4m3":
+        val = np.where((e == top) & (m == (1 << sp.mant_bits) - 1), np.nan, val)
+    elif fmt == "mxfp8_e5m2":
+        val = np.where(e == top, np.where(m == 0, sign * np.inf, np.nan), val)
+    return val
+
+
+def to_mfma(packed, scales, rows, cols, fmt):
+    """Codes and exponents of a block-32 tensor that the matrix cores decode
+    to the reference's values: an FP8 block holding an all-ones-exponent code
+    is written one binade lower (every value / 2) with exponent s + 1, unless
+    s is already 127; a value of an odd number of smallest-subnormal units at
+    the new exponent rounds half to even.  Returns (packed, scales, rounded)."""
+    sp = SPECS[fmt]
+    scales = np.asarray(scales, np.int8).reshape(rows, cols // 32).copy()
+    if sp.bits != 8:
+        return np.asarray(packed, np.uint8).copy(), scales, 0
+    codes = np.asarray(packed, np.uint8).reshape(rows, cols // 32, 32).astype(np.int64)
+    mb = sp.mant_bits
+    e = (codes & 0x7F) >> mb
+    ref_only = e == (1 << sp.exp_bits) - 1
+    if fmt == "mxfp8_e4m3":
+        ref_only &= (codes & ((1 << mb) - 1)) == (1 << mb) - 1
+    fix = ref_only.any(axis=-1) & (scales.astype(np.int64) < 127)
+    sign, mag = codes & 0x80, codes & 0x7F
+    m = mag & ((1 << mb) - 1)
+    k = np.where(e == 0, m, (1 << mb) + m)            # value in smallest-subnormal units (fields 0, 1)
+    h = k >> 1
+    h = h + ((k & 1) & (h & 1))                       # half to even
+    halved = np.where(e >= 2, mag - (1 << mb), h) | sign
+    out = np.where(fix[..., None], halved, codes).astype(np.uint8)
+    rounded = int(((e < 2) & (k & 1).astype(bool) & fix[..., None]).sum())
+    scales = np.where(fix, scales.astype(np.int64) + 1, scales).astype(np.int8)
+    return out.reshape(-1), scales, rounded

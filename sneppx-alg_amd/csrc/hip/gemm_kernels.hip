@@ -453,6 +453,188 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
     }
 }
 
+// MXFP8 / MXFP6 x the same format (block 32 along K, one E8M0 exponent per
+// block) on v_mfma_scale_f32_16x16x128_f8f6f4: the fp8 kernel's 256 x 224
+// tiles and 8 waves of 64 x 112, K stages of 128 elements (one MFMA step),
+// double buffered, with each stage's scale bytes of every tile row (4 per
+// row) staged beside it.  MF is the matrix cores' element format (0 e4m3,
+// 1 e5m2, 2 e2m3, 3 e3m2), EB its bits.  A row of a stage is 128 * EB / 8
+// bytes (8 or 6 chunks of 16 B); its chunks go to the XOR-swizzled slots of a
+// 128-byte LDS row, and the two padding slots of an fp6 row load a chunk the
+// same instruction loads anyway (no extra memory traffic; never read).
+// Lane (r16, q) carries the exponent of block q of the stage (elements
+// [32 q, +32)) as its MFMA scale.  Its operand registers hold, for fp6, that
+// block (24 bytes, packed little-endian as the reference writes them); for
+// fp8, elements [16 q, +16) in registers 0-3 and [64 + 16 q, +16) in 4-7 --
+// the matrix cores' 8-bit k order, in which register half h of lane group q
+// is scaled by the exponent of lane group 2 h + q / 2.  fp8 codes must be decodable by the
+// matrix cores (no all-ones exponents: see k_mx_to_mfma).
+constexpr int MX8_SCALES = 512;                          // scale dwords per stage (480 used)
+constexpr int MX8_STAGE = TLDS_STAGE + MX8_SCALES * 4;
+
+template <int MF, int EB, bool YF32>
+__global__ void __launch_bounds__(512) k_mx8_tiled(const uint8_t* __restrict__ A,
+                                                   const int8_t* __restrict__ sA,
+                                                   const uint8_t* __restrict__ W,
+                                                   const int8_t* __restrict__ sW,
+                                                   void* __restrict__ out, int M, int N, int K,
+                                                   int tiles_m, int tiles_n) {
+    constexpr int FM = 4;
+    constexpr int RB = 128 * EB / 8, NCH = RB / 16;      // bytes and chunks of a row per stage
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, q = lane >> 4;
+
+    const int b = blockIdx.x, nb = gridDim.x;
+    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int m0 = tm * TBM, n0 = tn * TBN;
+    const uint32_t KB = (uint32_t)K * EB / 8, KS = (uint32_t)K / 32;   // code and scale bytes per row
+
+    // LDS slot lslot of row r holds chunk lslot ^ swz(r); padding slots of an
+    // fp6 row (chunk >= 6) repeat chunk c - 4 of the same row
+    const int lrow = lane >> 3, lslot = lane & 7;
+    uint32_t ga[4], gw[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int row = (8 * i + wave) * 8 + lrow;
+        const int gr = m0 + row < M ? m0 + row : M - 1;
+        int c = lslot ^ swz(row);
+        c = c < NCH ? c : c - 4;
+        ga[i] = (uint32_t)gr * KB + (uint32_t)c * 16u;
+        const int wr = row < TBN ? row : TBN - 1;
+        const int gn = n0 + wr < N ? n0 + wr : N - 1;
+        int cw = lslot ^ swz(wr);
+        cw = cw < NCH ? cw : cw - 4;
+        gw[i] = (uint32_t)gn * KB + (uint32_t)cw * 16u;
+    }
+    // scale dword of tile row d = 64 wave + lane (A rows, then W rows; d >= 480 repeats row 479)
+    uint32_t gs;
+    bool s_is_a;
+    {
+        const int d = 64 * wave + lane < TBM + TBN ? 64 * wave + lane : TBM + TBN - 1;
+        s_is_a = d < TBM;
+        if (s_is_a) {
+            const int gr = m0 + d < M ? m0 + d : M - 1;
+            gs = (uint32_t)gr * KS;
+        } else {
+            const int gn = n0 + (d - TBM) < N ? n0 + (d - TBM) : N - 1;
+            gs = (uint32_t)gn * KS;
+        }
+    }
+    const __amdgpu_buffer_rsrc_t ra = brsrc(A), rw = brsrc(W), rsa = brsrc(sA), rsw = brsrc(sW);
+    auto dload = [&](int buf, int kt) {
+        int8_t* base = lds + buf * MX8_STAGE;
+        const uint32_t k0 = (uint32_t)kt * RB;
+#pragma unroll
+        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
+#pragma unroll
+        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
+        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
+        // wave-uniform operand choice (waves 0-3 hold A rows, 4-7 W rows)
+        if (wave < 4)
+            bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs, 4u * (uint32_t)kt);
+        else
+            bload_lds(rsw, base + TLDS_STAGE + wave * 256, 4, gs, 4u * (uint32_t)kt);
+    };
+
+    f32x4 acc[FM][TFN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < TFN; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int sw = swz(r16);
+    const int8_t* arow = lds + (wm * 64 + r16) * TBK;
+    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
+    const int8_t* srow_a = lds + TLDS_STAGE + (wm * 64 + r16) * 4 + q;
+    const int8_t* srow_w = lds + TLDS_STAGE + (TBM + wn * 112 + r16) * 4 + q;
+    const int nk = K / 128;
+
+    // lane group q's operand: fp8 chunks q and q + 4 of the row; fp6 block q
+    auto frag = [&](const int8_t* row) -> i32x8 {
+        if (EB == 8) {
+            const i32x4 lo = lds16(row + ((q ^ sw) << 4));
+            const i32x4 hi = lds16(row + (((q + 4) ^ sw) << 4));
+            return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        } else {
+            typedef int i32x2 __attribute__((ext_vector_type(2)));
+            i32x2 p[3];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const int byte = 24 * q + 8 * j;
+                p[j] = *reinterpret_cast<const i32x2*>(row + ((((byte >> 4) ^ sw) << 4) | (byte & 15)));
+            }
+            return i32x8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], 0, 0};
+        }
+    };
+
+    dload(0, 0);
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
+        __syncthreads();
+        dload(cur ^ 1, kt + 1 < nk ? kt + 1 : 0);   // last stage: stage 0 again, unused
+        const int8_t* ab = arow + cur * MX8_STAGE;
+        const int8_t* wb = wrow + cur * MX8_STAGE;
+        i32x8 fa[FM], fw[TFN];
+        int sca[FM], scw[TFN];
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            fa[i] = frag(ab + i * 16 * TBK);
+            sca[i] = e8m0_of(srow_a[cur * MX8_STAGE + i * 16 * 4]);
+        }
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            fw[j] = frag(wb + j * 16 * TBK);
+            scw[j] = e8m0_of(srow_w[cur * MX8_STAGE + j * 16 * 4]);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < TFN; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                    fa[i], fw[j], acc[i][j], MF, MF, 0, sca[i], 0, scw[j]);
+    }
+    __builtin_amdgcn_s_waitcnt(0x0070);   // the last (unused) loads drain before exit
+
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            const int n = n0 + wn * 112 + j * 16 + r16;
+            if (n >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+                if (m >= M) continue;
+                if (YF32)
+                    reinterpret_cast<float*>(out)[(size_t)m * N + n] = acc[i][j][e];
+                else
+                    reinterpret_cast<uint16_t*>(out)[(size_t)m * N + n] = bf16_out(acc[i][j][e]);
+            }
+        }
+    }
+}
+
+template <int MF, int EB, bool YF32>
+int launch_mx8_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                     void* out, int M, int N, int K, hipStream_t st) {
+    const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
+    const size_t lds = 2 * (size_t)MX8_STAGE;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_mx8_tiled<MF, EB, YF32>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("mx gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
+    }
+    k_mx8_tiled<MF, EB, YF32><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m,
+                                                                    tiles_n);
+    return snx_launch_check("k_mx8_tiled");
+}
+
 template <bool YF32>
 int launch_mxfp4_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                        void* out, int M, int N, int K, hipStream_t st) {
@@ -932,6 +1114,26 @@ int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W,
     }
     if (y_f32) return launch_mxfp4_tiled<true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
     return launch_mxfp4_tiled<false>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+}
+
+int snx_k_mx8_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                   void* out, int y_f32, int mf, size_t M, size_t N, size_t K, void* st) {
+    const int eb = mf < 2 ? 8 : 6;
+    if (K % 128 != 0 || (uint64_t)M * K * eb / 8 >= (1ull << 32) || (uint64_t)N * K * eb / 8 >= (1ull << 32)) {
+        snx_set_error("mx gemm: K %% 128 == 0 and operands below 4 GiB are required");
+        return -1;
+    }
+    const int m = (int)M, n = (int)N, k = (int)K;
+#define SNX_MX8(F, B)                                                                       \
+    return y_f32 ? launch_mx8_tiled<F, B, true>(A, sA, W, sW, out, m, n, k, S(st))          \
+                 : launch_mx8_tiled<F, B, false>(A, sA, W, sW, out, m, n, k, S(st))
+    switch (mf) {
+        case 0: SNX_MX8(0, 8);
+        case 1: SNX_MX8(1, 8);
+        case 2: SNX_MX8(2, 6);
+        default: SNX_MX8(3, 6);
+    }
+#undef SNX_MX8
 }
 
 int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const float* sW,

@@ -276,6 +276,79 @@ unsigned grid_of(size_t items) {
     return (unsigned)(g ? g : 1);
 }
 
+// One code one binade lower (value / 2) in the same 8-bit format, MB mantissa
+// bits: fields >= 2 lose one exponent step exactly; field 1 and subnormals
+// become subnormals k / 2 (k = the value in units of the smallest subnormal),
+// rounded half to even when k is odd.  Returns the code; *inexact counts the
+// rounded ones.
+template <int MB>
+__device__ inline uint32_t half_code(uint32_t c, int* inexact) {
+    const uint32_t sign = c & 0x80u, mag = c & 0x7Fu, e = mag >> MB, m = mag & ((1u << MB) - 1u);
+    if (e >= 2) return sign | (mag - (1u << MB));
+    const uint32_t k = e ? (1u << MB) + m : m;          // value in subnormal units
+    uint32_t h = k >> 1;
+    if (k & 1u) {
+        h += h & 1u;
+        (*inexact)++;
+    }
+    return sign | h;    // h <= 2^MB: a subnormal, or exactly the smallest normal
+}
+
+// Reference MXFP8 blocks -> codes the gfx950 matrix cores decode to the same
+// values (OCP e4m3fn / e5m2 have no finite all-ones exponent, the reference
+// has: E4M3 0x7F = 480, E5M2 field 31 = 65536 .. 114688).  A block holding
+// such a code is re-encoded one binade lower with exponent s + 1 (exact but
+// for odd subnormal-unit values at the new scale, which round half to even);
+// other blocks are copied.  One thread per 32-element block; F 0 = e4m3,
+// 1 = e5m2.  A block at the largest exponent (127) stays as it is.
+template <int F>
+__global__ void __launch_bounds__(256) k_mx_to_mfma(const uint8_t* __restrict__ in,
+                                                    const int8_t* __restrict__ sin,
+                                                    uint8_t* __restrict__ out,
+                                                    int8_t* __restrict__ sout, size_t nblocks,
+                                                    unsigned int* __restrict__ rounded) {
+    constexpr int MB = F == 0 ? 3 : 2;
+    const size_t b = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (b >= nblocks) return;
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 v[2];
+    v[0] = reinterpret_cast<const u32x4*>(in + b * 32)[0];
+    v[1] = reinterpret_cast<const u32x4*>(in + b * 32)[1];
+    const int s = sin[b];
+    uint32_t any = 0;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t w = v[i][e];
+            if (F == 0)   // a byte whose low 7 bits are all ones carries into bit 7
+                any |= ((w & 0x7F7F7F7Fu) + 0x01010101u) & 0x80808080u;
+            else          // exponent field 31
+                any |= ((w & 0x7C7C7C7Cu) + 0x04040404u) & 0x80808080u;
+        }
+    if (!any || s >= 127) {
+        reinterpret_cast<u32x4*>(out + b * 32)[0] = v[0];
+        reinterpret_cast<u32x4*>(out + b * 32)[1] = v[1];
+        sout[b] = (int8_t)s;
+        return;
+    }
+    int inexact = 0;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const uint32_t w = v[i][e];
+            uint32_t r = 0;
+#pragma unroll
+            for (int j = 0; j < 4; j++) r |= half_code<MB>((w >> (8 * j)) & 0xFFu, &inexact) << (8 * j);
+            v[i][e] = r;
+        }
+    reinterpret_cast<u32x4*>(out + b * 32)[0] = v[0];
+    reinterpret_cast<u32x4*>(out + b * 32)[1] = v[1];
+    sout[b] = (int8_t)(s + 1);
+    if (inexact && rounded) atomicAdd(rounded, (unsigned)inexact);
+}
+
 }  // namespace
 
 extern "C" {
@@ -321,6 +394,15 @@ int snx_k_mx_quant_tensor(const float* x, uint8_t* packed, size_t n, int s, int 
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* st) {
     k_mx_dequant_tensor<<<grid_of(n), 256, 0, S(st)>>>(packed, y, n, s, f);
     return snx_launch_check("k_mx_dequant_tensor");
+}
+
+int snx_k_mx_to_mfma(const uint8_t* in, const int8_t* sin, uint8_t* out, int8_t* sout,
+                     size_t nblocks, int f, unsigned int* rounded, void* st) {
+    if (f == 0)
+        k_mx_to_mfma<0><<<grid_of(nblocks), 256, 0, S(st)>>>(in, sin, out, sout, nblocks, rounded);
+    else
+        k_mx_to_mfma<1><<<grid_of(nblocks), 256, 0, S(st)>>>(in, sin, out, sout, nblocks, rounded);
+    return snx_launch_check("k_mx_to_mfma");
 }
 
 }  // extern "C"

@@ -132,3 +132,89 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
         return snx_k_mxfp4_gemm_tiled(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
     return snx_k_mxfp4_gemm(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
 }
+
+/* MFMA element format of an MX format: 0 e4m3, 1 e5m2, 2 e2m3, 3 e3m2, 4 e2m1 */
+static int mfma_fmt(SNEPPXMXFormat f) {
+    switch (f) {
+        case SNEPPX_MXFP8_E4M3: return 0;
+        case SNEPPX_MXFP8_E5M2: return 1;
+        case SNEPPX_MXFP6_E2M3: return 2;
+        case SNEPPX_MXFP6_E3M2: return 3;
+        case SNEPPX_MXFP4_E2M1: return 4;
+        default: return -1;
+    }
+}
+
+int SNEPPX_mx_to_mfma(const uint8_t* packed, const int8_t* scales, uint8_t* out_packed,
+                      int8_t* out_scales, size_t rows, size_t cols, SNEPPXMXFormat fmt,
+                      unsigned int* rounded, SNEPPXStream stream) {
+    REQUIRE(packed && scales && out_packed && out_scales, "mx_to_mfma: NULL pointer");
+    REQUIRE(rows && cols, "mx_to_mfma: empty tensor");
+    REQUIRE(mfma_fmt(fmt) >= 0, "mx_to_mfma: format %d has no block-32 matrix-core form", (int)fmt);
+    REQUIRE(cols % 32 == 0, "mx_to_mfma: cols=%zu must be a multiple of the block (32)", cols);
+    snx_clear_error();
+    const size_t nblocks = rows * (cols / 32);
+    if (fmt == SNEPPX_MXFP8_E4M3 || fmt == SNEPPX_MXFP8_E5M2) {
+        REQUIRE(((uintptr_t)packed & 15u) == 0 && ((uintptr_t)out_packed & 15u) == 0,
+                "mx_to_mfma: code buffers must be 16-byte aligned");
+        return snx_k_mx_to_mfma(packed, scales, out_packed, out_scales, nblocks,
+                                fmt == SNEPPX_MXFP8_E5M2, rounded, stream);
+    }
+    /* fp6 / fp4: the reference's codes are the matrix cores' own */
+    int rc = snx_hip_memcpy_d2d(out_packed, packed, nblocks * 32 * (size_t)k_bits[fmt] / 8, stream);
+    if (!rc) rc = snx_hip_memcpy_d2d(out_scales, scales, nblocks, stream);
+    return rc;
+}
+
+static int mx_gemm_check(const char* who, const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                         const int8_t* sW, SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype,
+                         size_t M, size_t N, size_t K) {
+    REQUIRE(A && sA && W && sW && out, "%s: NULL pointer", who);
+    REQUIRE(M && N && K, "%s: empty shape", who);
+    REQUIRE(mfma_fmt(fmt) >= 0, "%s: format %d has no block-32 matrix-core form", who, (int)fmt);
+    REQUIRE(out_dtype == SNEPPX_BFLOAT16 || out_dtype == SNEPPX_FLOAT32,
+            "%s: out_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32", who);
+    REQUIRE(((uintptr_t)A & 15u) == 0 && ((uintptr_t)W & 15u) == 0, "%s: A and W must be 16-byte aligned",
+            who);
+    if (fmt != SNEPPX_MXFP4_E2M1) {
+        REQUIRE(K % 128 == 0, "%s: K=%zu must be a multiple of 128", who, K);
+        REQUIRE(((uintptr_t)sA & 3u) == 0 && ((uintptr_t)sW & 3u) == 0,
+                "%s: the exponent arrays must be 4-byte aligned", who);
+    }
+    return 0;
+}
+
+int SNEPPX_qlinear_mx_gemm_mfma(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                                const int8_t* sW, SNEPPXMXFormat fmt, void* out,
+                                SNEPPXDtype out_dtype, size_t M, size_t N, size_t K,
+                                SNEPPXStream stream) {
+    if (mx_gemm_check("qlinear_mx_gemm_mfma", A, sA, W, sW, fmt, out, out_dtype, M, N, K)) return -1;
+    snx_clear_error();
+    if (fmt == SNEPPX_MXFP4_E2M1)
+        return SNEPPX_qlinear_mxfp4_gemm(A, sA, W, sW, out, out_dtype, M, N, K, stream);
+    return snx_k_mx8_gemm(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, mfma_fmt(fmt), M, N, K,
+                          stream);
+}
+
+int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                           SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype, size_t M,
+                           size_t N, size_t K, SNEPPXStream stream) {
+    if (mx_gemm_check("qlinear_mx_gemm", A, sA, W, sW, fmt, out, out_dtype, M, N, K)) return -1;
+    snx_clear_error();
+    if (fmt != SNEPPX_MXFP8_E4M3 && fmt != SNEPPX_MXFP8_E5M2)
+        return SNEPPX_qlinear_mx_gemm_mfma(A, sA, W, sW, fmt, out, out_dtype, M, N, K, stream);
+    /* fp8: both operands through the conversion into the calling thread's workspace */
+    const size_t ab = (M * K + 255) & ~(size_t)255, wb = (N * K + 255) & ~(size_t)255;
+    const size_t asb = (M * (K / 32) + 255) & ~(size_t)255;
+    uint8_t* ws = (uint8_t*)snx_workspace(ab + wb + asb + N * (K / 32), 0, stream);
+    if (!ws) return -1;
+    uint8_t* a2 = ws;
+    uint8_t* w2 = ws + ab;
+    int8_t* sa2 = (int8_t*)(ws + ab + wb);
+    int8_t* sw2 = (int8_t*)(ws + ab + wb + asb);
+    int rc = SNEPPX_mx_to_mfma(A, sA, a2, sa2, M, K, fmt, NULL, stream);
+    if (!rc) rc = SNEPPX_mx_to_mfma(W, sW, w2, sw2, N, K, fmt, NULL, stream);
+    if (!rc) rc = snx_k_mx8_gemm(a2, sa2, w2, sw2, out, out_dtype == SNEPPX_FLOAT32, mfma_fmt(fmt), M, N,
+                                 K, stream);
+    return rc;
+}

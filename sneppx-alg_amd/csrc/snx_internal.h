@@ -82,6 +82,14 @@ int snx_k_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const
 int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                            void* out, int y_f32, size_t M, size_t N, size_t K, void* st);
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* stream);
+/* reference MXFP8 blocks (f 0 e4m3, 1 e5m2) -> matrix-core-decodable codes and
+ * exponents; *rounded (device, may be NULL) counts elements that rounded */
+int snx_k_mx_to_mfma(const uint8_t* in, const int8_t* sin, uint8_t* out, int8_t* sout,
+                     size_t nblocks, int f, unsigned int* rounded, void* stream);
+/* MXFP8 / MXFP6 GEMM on matrix-core-decodable operands; mf the MFMA element
+ * format (0 e4m3, 1 e5m2, 2 e2m3, 3 e3m2); K % 128 == 0 */
+int snx_k_mx8_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                   void* out, int y_f32, int mf, size_t M, size_t N, size_t K, void* stream);
 
 /* model-zoo int8 codes with the multiplier in rec[0] (weights.c:242-247) */
 int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,

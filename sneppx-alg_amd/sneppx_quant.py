@@ -134,6 +134,9 @@ EXPORTS = {
     "SNEPPX_dev_quantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
     "SNEPPX_dev_dequantize_mx": (C.c_int, [_vp, _vp, _vp, _sz, _sz, C.c_int, C.c_int, _vp]),
     "SNEPPX_qlinear_mxfp4_gemm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_mx_gemm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_mx_gemm_mfma": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _sz, _sz, _sz, _vp]),
+    "SNEPPX_mx_to_mfma": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp, _vp]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
     "snx_hip_event_create": (C.c_int, [C.POINTER(_vp)]),
@@ -502,6 +505,25 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_mxfp4_gemm"](
             _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(out), ydt, M, N, K, self._stream(stream)),
             "qlinear_mxfp4_gemm")
+
+    def qlinear_mx_gemm(self, A, sA, W, sW, fmt, out, M, N, K, stream=None, mfma_form=False):
+        """out = A W^T for block-32 MX operands of format `fmt` (FP8 / FP6 / FP4);
+        mfma_form: operands already converted by mx_to_mfma."""
+        ydt = SNEPPX_FLOAT32 if out.dtype == torch.float32 else SNEPPX_BFLOAT16
+        name = "SNEPPX_qlinear_mx_gemm_mfma" if mfma_form else "SNEPPX_qlinear_mx_gemm"
+        self.check(self.fn[name](
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), MX_FORMATS.index(fmt), _ptr(out), ydt, M, N, K,
+            self._stream(stream)), name[7:])
+
+    def mx_to_mfma(self, packed, scales, rows, cols, fmt, stream=None):
+        """(packed, scales, rounded) in the matrix cores' encoding; rounded is an
+        int32 device counter of the elements that rounded half to even."""
+        out_p, out_s = torch.empty_like(packed), torch.empty_like(scales)
+        rounded = torch.zeros(1, dtype=torch.int32, device=packed.device)
+        self.check(self.fn["SNEPPX_mx_to_mfma"](
+            _ptr(packed), _ptr(scales), _ptr(out_p), _ptr(out_s), rows, cols, MX_FORMATS.index(fmt),
+            _ptr(rounded), self._stream(stream)), "mx_to_mfma")
+        return out_p, out_s, rounded
 
     # ---------------- HIP events on an explicit stream ----------------------
     def event(self):

@@ -115,3 +115,105 @@ def test_mxfp4_gemm_rejects_k_not_multiple_of_64(lib):
     s = torch.zeros(8, dtype=torch.int8, device=DEV)
     with pytest.raises(Exception, match="multiple of 64"):
         lib.qlinear_mxfp4_gemm(z, s, z, s, torch.empty((2, 2), device=DEV), 2, 2, 96)
+
+
+MX_BLOCK32 = ["mxfp8_e4m3", "mxfp8_e5m2", "mxfp6_e3m2", "mxfp6_e2m3"]
+
+
+def _mx_operand(rng, rows, K, spread):
+    x = rng.normal(0, 1, (rows, K)) * 10.0 ** rng.integers(-spread, spread + 1, (rows, 1))
+    return x.astype(np.float32)
+
+
+def _mfma_values(packed, scales, rows, K, fmt):
+    """float64 values of the matrix-core form of a reference MX tensor: the
+    oracle's re-encoding, decoded as the OCP format (FP6: the reference's own
+    codes and decode)."""
+    p2, s2, _ = mx.to_mfma(packed, scales, rows, K, fmt)
+    sp = mx.SPECS[fmt]
+    if sp.bits != 8:
+        return mx.dequantize(p2, s2, (rows, K), fmt).astype(np.float64)
+    v = mx.ocp_decode(p2.astype(np.int64), fmt).reshape(rows, K // 32, 32)
+    return (v * 2.0 ** s2.astype(np.float64)[..., None]).reshape(rows, K)
+
+
+@pytest.mark.parametrize("fmt", MX_BLOCK32)
+def test_to_mfma_bit_exact(lib, fmt):
+    print(f"[gpu] mx_to_mfma {fmt}", flush=True)
+    rng = np.random.default_rng(7)
+    rows, cols = 96, 1024
+    x = _mx_operand(rng, rows, cols, 3)
+    x[0, :32] = 480.0 / 7     # a block whose peak lands on the format's largest element
+    p, s = lib.dev_quantize_mx(torch.from_numpy(x).to(DEV), fmt)
+    p2, s2, rounded = lib.mx_to_mfma(p, s, rows, cols, fmt)
+    torch.cuda.synchronize()
+    ep, es, er = mx.to_mfma(p.cpu().numpy(), s.cpu().numpy(), rows, cols, fmt)
+    assert np.array_equal(p2.cpu().numpy().reshape(-1), ep)
+    assert np.array_equal(s2.cpu().numpy().reshape(es.shape), es)
+    assert int(rounded.item()) == er
+    if mx.SPECS[fmt].bits == 8:
+        assert not np.array_equal(es, s.cpu().numpy().reshape(es.shape))
+
+
+@pytest.mark.parametrize("fmt", MX_BLOCK32)
+@pytest.mark.parametrize("M,N,K", [(256, 224, 128), (300, 500, 384), (1, 17, 256), (513, 449, 1024)])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_mx_gemm_against_dequantized_product(lib, fmt, M, N, K, out):
+    """MXFP8 / MXFP6 GEMM on the scaled matrix cores against the float64
+    product of the operands' matrix-core values (the oracle's re-encoding),
+    which lies within 1e-6 of the reference's own dequantized product."""
+    print(f"[gpu] mx gemm {fmt} M={M} N={N} K={K} {out}", flush=True)
+    rng = np.random.default_rng(M + 3 * N + K)
+    a, w = _mx_operand(rng, M, K, 1), _mx_operand(rng, N, K, 2) * 0.02
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(a).to(DEV), fmt)
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(w).to(DEV), fmt)
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_mx_gemm(pa, sa, pw, sw, fmt, y, M, N, K)
+    torch.cuda.synchronize()
+    hpa, hsa, hpw, hsw = (t.cpu().numpy() for t in (pa, sa, pw, sw))
+    va, vw = _mfma_values(hpa, hsa, M, K, fmt), _mfma_values(hpw, hsw, N, K, fmt)
+    ref = va @ vw.T
+    got = y.float().cpu().numpy().astype(np.float64)
+    if out == "f32":
+        # exact products; the scaled matrix cores sum each 128-element step
+        # keeping about 16 bits relative to its sum of |products| (measured
+        # 2.1e-5 of sum |a_k w_k| for the FP8 and E3M2 formats, 0 for E2M3),
+        # then add it to the fp32 accumulator: bound 2^-13 sum_k |a_k w_k|
+        absprod = np.abs(va) @ np.abs(vw).T
+        rel = (np.abs(got - ref) / np.maximum(absprod, 1e-300)).max()
+        print(f"[gpu]   max |err| / sum|a w| = {rel:.3g}", flush=True)
+        assert rel <= 2.0 ** -13, rel
+    else:
+        assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-2
+    # the re-encoding moves the reference's own product by far less than that
+    refd = mx.dequantize(hpa, hsa, (M, K), fmt) @ mx.dequantize(hpw, hsw, (N, K), fmt).T
+    assert np.abs(ref - refd).max() <= 1e-6 * np.abs(refd).max()
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8_e4m3", "mxfp6_e2m3"])
+def test_mx_gemm_on_weights_kept_in_matrix_core_form(lib, fmt):
+    """Weights converted once (mx_to_mfma) and the activations per call give
+    the same bits as the converting entry point."""
+    print(f"[gpu] mx gemm mfma-form {fmt}", flush=True)
+    rng = np.random.default_rng(11)
+    M, N, K = 130, 260, 512
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(_mx_operand(rng, M, K, 1)).to(DEV), fmt)
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(_mx_operand(rng, N, K, 1)).to(DEV), fmt)
+    y1 = torch.empty((M, N), device=DEV)
+    y2 = torch.empty_like(y1)
+    lib.qlinear_mx_gemm(pa, sa, pw, sw, fmt, y1, M, N, K)
+    a2, sa2, _ = lib.mx_to_mfma(pa, sa, M, K, fmt)
+    w2, sw2, _ = lib.mx_to_mfma(pw, sw, N, K, fmt)
+    lib.qlinear_mx_gemm(a2, sa2, w2, sw2, fmt, y2, M, N, K, mfma_form=True)
+    torch.cuda.synchronize()
+    assert torch.equal(y1, y2)
+
+
+def test_mx_gemm_rejects_bad_shapes(lib):
+    z = torch.zeros(4096, dtype=torch.uint8, device=DEV)
+    s = torch.zeros(128, dtype=torch.int8, device=DEV)
+    y = torch.empty((2, 2), device=DEV)
+    with pytest.raises(Exception, match="multiple of 128"):
+        lib.qlinear_mx_gemm(z, s, z, s, "mxfp8_e4m3", y, 2, 2, 96)
+    with pytest.raises(Exception, match="block-32"):
+        lib.qlinear_mx_gemm(z, s, z, s, "nvfp4_e2m1", y, 2, 2, 128)

@@ -101,3 +101,54 @@ def test_pack_unpack_bitstream():
         np.testing.assert_array_equal(mx.unpack(p, bits, 101), c)
     # 6-bit: codes 1, 2, 3, 4 -> bits 000001 000010 000011 000100, little end first
     assert mx.pack([1, 2, 3, 4], 6).tolist() == [0x81, 0x30, 0x10]
+
+
+@pytest.mark.parametrize("fmt", ["mxfp8_e4m3", "mxfp8_e5m2"])
+@pytest.mark.parametrize("seed", [0, 1])
+def test_to_mfma_keeps_every_value(fmt, seed):
+    """The matrix-core form decodes (as the OCP format) to the reference's
+    values: exactly, except the counted half-to-even elements, which move by
+    at most half a smallest subnormal at the new exponent; no code the
+    matrix cores would read as NaN or inf remains; untouched blocks keep
+    their bytes and exponent."""
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_t(3, (64, 512)) * 10.0 ** rng.integers(-3, 3, (64, 1))).astype(np.float32)
+    x[0, :32] = np.linspace(-1, 1, 32)
+    x[0, 5] = 480.0 / 7                      # scaled peak at the format's largest element
+    packed, scales = mx.quantize(x, fmt)
+    sp = mx.SPECS[fmt]
+    p2, s2, rounded = mx.to_mfma(packed, scales, 64, 512, fmt)
+    ref = mx.decode(packed.astype(np.int64), sp).reshape(64, 16, 32) * 2.0 ** scales.astype(np.float64)[..., None]
+    hw = mx.ocp_decode(p2.astype(np.int64), fmt).reshape(64, 16, 32) * 2.0 ** s2.astype(np.float64)[..., None]
+    assert np.isfinite(hw).all()
+    changed = s2 != scales
+    assert changed.any() and (s2[changed] == scales[changed] + 1).all()
+    same = ~changed
+    assert np.array_equal(p2.reshape(64, 16, 32)[same], packed.reshape(64, 16, 32)[same])
+    diff = np.abs(hw - ref)
+    unit = 2.0 ** (1 - sp.bias - sp.mant_bits) * 2.0 ** s2.astype(np.float64)[..., None]
+    assert (diff <= 0.5 * unit).all()
+    assert (diff > 0).sum() == rounded
+    # the reference-only codes are common: about one block in twenty for E4M3
+    assert changed.mean() > (0.01 if fmt == "mxfp8_e4m3" else 0.2)
+
+
+def test_to_mfma_known_answers():
+    # E4M3 block: 0x7F (480) and 0x7E (448) -> 0x77 (240) and 0x76 (224), s + 1;
+    # subnormal / smallest-normal halving: units k = 1, 3, 5, 7, 9, 15 -> 0, 2, 2, 4, 4, 8
+    blk = np.zeros(32, np.uint8)
+    blk[:8] = [0x7F, 0x7E, 0x01, 0x03, 0x05, 0x07, 0x09, 0x0F]
+    blk[8] = 0x80 | 0x7F
+    p2, s2, rounded = mx.to_mfma(blk, np.array([3], np.int8), 1, 32, "mxfp8_e4m3")
+    assert list(p2[:9]) == [0x77, 0x76, 0x00, 0x02, 0x02, 0x04, 0x04, 0x08, 0xF7]
+    assert s2[0, 0] == 4 and rounded == 6
+    assert mx.ocp_decode(np.array([0x7F, 0x77, 0x7E]), "mxfp8_e4m3")[1:].tolist() == [240.0, 448.0]
+    assert np.isnan(mx.ocp_decode(np.array([0x7F]), "mxfp8_e4m3")[0])
+    # E5M2 field 31 (65536 .. 114688 in the reference, inf / NaN in OCP) -> field 30
+    b5 = np.zeros(32, np.uint8)
+    b5[:3] = [0x7C, 0x7F, 0x05]
+    p5, s5, r5 = mx.to_mfma(b5, np.array([-2], np.int8), 1, 32, "mxfp8_e5m2")
+    assert list(p5[:3]) == [0x78, 0x7B, 0x02] and s5[0, 0] == -1 and r5 == 1
+    # a block at exponent 127 cannot move up and stays as it is
+    p7, s7, _ = mx.to_mfma(blk, np.array([127], np.int8), 1, 32, "mxfp8_e4m3")
+    assert np.array_equal(p7, blk) and s7[0, 0] == 127
