@@ -43,6 +43,12 @@ __device__ __forceinline__ u32x4 load16(const void* p) {
     return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Buffer loads: an offset at or past a buffer's record count returns zeros
+// and touches no memory; kNontemporal is the cache policy of a nontemporal
+// access (the "nt" bit).
+constexpr uint32_t kNoRecord = 0x7ffffff0u;
+constexpr int kNontemporal = 2;
+
 // ----------------------------------------------------------------- W8 GEMV
 // One wave per R rows; lane l covers bytes [16 l, 16 l + 16) of every
 // 1024-column slice, so a wave load instruction reads 1 KB contiguous.
@@ -525,8 +531,8 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
     }
 }
 
-// M = 1 decode GEMV, group 128, K = 2048 T.  A workgroup (8 waves) owns 16
-// output rows, each wave 2 of them; lane l of a wave covers the 32-column
+// M = 1 decode GEMV, group 128, K = 2048 T.  A workgroup (8 waves) owns an
+// even share of the N output rows (at most 16), each wave up to 2 of them; lane l of a wave covers the 32-column
 // chunks c = 64 t + l (16 bytes of a row, one 16-byte load), so a wave load
 // instruction reads 1 KB of one row and the lane's columns are the same for
 // both rows.  The product runs on v_mfma_f32_4x4x4bf16_1k with only its
@@ -548,7 +554,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
                                                      const uint32_t* __restrict__ qz,
                                                      const uint16_t* __restrict__ perm,
                                                      void* __restrict__ y,
-                                                     const float* __restrict__ bias, int N) {
+                                                     const float* __restrict__ bias, int N,
+                                                     int rows_q, int rows_rem) {
     constexpr int K = 2048 * T, G = 16 * T, KW = K / 8, NCH = K / 32, NIT = K / 8;
     constexpr int RW = 2, WROWS = 16, NTHR = 512;
     constexpr int XPT = (NIT + NTHR - 1) / NTHR;
@@ -562,7 +569,13 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wg0 = blockIdx.x * WROWS;
+    // rows [wg0, rend) of this workgroup: an even share of N (rows_q or
+    // rows_q + 1 <= WROWS; rows_q = N / grid, rows_rem = N % grid), so every
+    // CU gets the same number of rows when the grid is a multiple of the CU
+    // count
+    const int b = blockIdx.x;
+    const int wg0 = b * rows_q + (b < rows_rem ? b : rows_rem);
+    const int rend = wg0 + rows_q + (b < rows_rem ? 1 : 0);
     const int n0 = wg0 + wave * RW;
 
     // 1. activations (and perm), then the raw scales / zero words of the 16 rows
@@ -580,28 +593,34 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     const bool zload = ZEROS && tid >= WROWS * SPR && tid < WROWS * (SPR + ZPR);
     if (sload) {
         int row = wg0 + tid / SPR;
-        row = row < N ? row : N - 1;
+        row = row < rend ? row : rend - 1;
         sv = load16(scales + (size_t)row * G + (tid % SPR) * 8);
     }
     if (zload) {
         const int j = tid - WROWS * SPR;
         int row = wg0 + j / ZPR;
-        row = row < N ? row : N - 1;
+        row = row < rend ? row : rend - 1;
         zv = qz[(size_t)row * ZPR + j % ZPR];
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 
-    // 2. weights: RW rows x T chunks, all in flight
+    // 2. weights: RW rows x T chunks, all in flight (nontemporal).  A row past
+    // the workgroup's share reads zeros without a memory access: its offset
+    // lies beyond the buffer's record count.
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(qw), (short)0, N * KW * 4, 0x00020000);
     u32x4 wv[RW][T];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        int row = n0 + r < N ? n0 + r : N - 1;
+        const bool live = n0 + r < rend;
 #pragma unroll
-        for (int t = 0; t < T; t++)
-            wv[r][t] = __builtin_nontemporal_load(
-                reinterpret_cast<const u32x4*>(qw + (size_t)row * KW + (64 * t + lane) * 4));
+        for (int t = 0; t < T; t++) {
+            const uint32_t off = live ? (uint32_t)(n0 + r) * (KW * 4) + (uint32_t)(64 * t + lane) * 16u
+                                      : kNoRecord;
+            wv[r][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, kNontemporal));
+        }
     }
     asm volatile("" ::: "memory");
 
@@ -727,7 +746,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     if (lane == 63) {
 #pragma unroll
         for (int r = 0; r < RW; r++) {
-            if (n0 + r >= N) break;
+            if (n0 + r >= rend) break;
             if (bias) out[r] += bias[n0 + r];
             if (YF32)
                 reinterpret_cast<float*>(y)[n0 + r] = out[r];
@@ -924,9 +943,19 @@ size_t gemv1_lds(size_t K, bool perm) {
     return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
 }
 
+// Workgroups of the M = 1 kernel: enough for at most 16 rows each, rounded up
+// to a multiple of the CU count once there is more than one per CU, so each
+// workgroup takes an even share of the rows and every CU the same number.
+unsigned gemv1_grid(int N) {
+    const int ncu = snx::cu_count();
+    int nwg = (N + 15) / 16;
+    if (nwg > ncu) nwg = (nwg + ncu - 1) / ncu * ncu;
+    return (unsigned)(nwg < N ? nwg : N);
+}
+
 template <int T, bool PERM>
 int launch_gemv1_t(const W4Launch& a) {
-    dim3 grid((unsigned)((a.N + 15) / 16)), block(512);
+    dim3 grid(gemv1_grid(a.N)), block(512);
     const size_t lds = gemv1_lds((size_t)a.K, PERM);
     if (lds > 64 * 1024) {   // PERM at K > 8192: the staged copies of x and perm
         static std::atomic<uint64_t> lds_done[4];   // (zeros, f32 out) variants, per device
@@ -942,7 +971,8 @@ int launch_gemv1_t(const W4Launch& a) {
     }
 #define SNX_G1(Z, F)                                                                      \
     k_w4a16_gemv1<T, Z, F, PERM><<<grid, block, lds, a.s>>>(a.x, a.qw, a.scales, a.qz, a.perm, \
-                                                            a.y, a.bias, a.N)
+                                                            a.y, a.bias, a.N, a.N / (int)grid.x, \
+                                                            a.N % (int)grid.x)
     if (a.qz) {
         if (a.y_f32) SNX_G1(true, true);
         else SNX_G1(true, false);
@@ -956,7 +986,8 @@ int launch_gemv1_t(const W4Launch& a) {
 
 bool gemv1_ok(const W4Launch& a) {
     return a.M == 1 && a.group == 128 && a.K % 2048 == 0 && a.K <= 16384 &&
-           ((uintptr_t)a.scales & 15u) == 0 && ((uintptr_t)a.qz & 3u) == 0;
+           ((uintptr_t)a.scales & 15u) == 0 && ((uintptr_t)a.qz & 3u) == 0 &&
+           (uint64_t)a.N * (uint64_t)a.K / 2 < kNoRecord;   // buffer offsets of the weights
 }
 
 template <bool PERM>
