@@ -47,7 +47,7 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "decode", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -115,7 +115,7 @@ def bench_loops():
         path = os.path.join(REPO, "sneppx-alg_amd", "libsneppx_bench.so")
         _BENCHLIB = C.CDLL(path) if os.path.exists(path) else False
         if _BENCHLIB:
-            for name in ("snxb_loop_w4a16", "snxb_loop_w4a16_actorder", "snxb_loop_w8_gemv"):
+            for name in ("snxb_loop_w4a16", "snxb_loop_w4a16_actorder", "snxb_loop_w8_gemv", "snxb_loop_decode"):
                 getattr(_BENCHLIB, name).restype = C.c_int
     return _BENCHLIB or None
 
@@ -183,6 +183,55 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
         "launch_ms_median": med_launch, "gbs": nbytes / (total / steps) / 1e6,
         "gbs_kernel": nbytes / mean_launch / 1e6,
     }, (ws, x, y, G)
+
+
+LLAMA3_LINEARS = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
+
+
+def bench_decode(lib, timer, torch, copies, steps, warmup, layer):
+    """One token (M = 1) through C5's Llama-3-8B linears: the gate/up
+    projection with its SwiGLU step as one launch (layer False), or the
+    layer's four linears back to back (QKV, O, gate/up + SwiGLU, down; the
+    attention and norms between them are not part of it), weights rotated
+    over `copies` copies so they stream from HBM."""
+    H, F = 4096, 14336
+    names = list(LLAMA3_LINEARS) if layer else ["gate_up"]
+    ws = {}
+    for i, (n, (N, K)) in enumerate(LLAMA3_LINEARS.items()):
+        if n in names:
+            ws[n], _ = make_w4(lib, N, K, 128, copies, 40 + i, torch)
+    g = torch.Generator(device="cuda").manual_seed(47)
+    x = torch.randn((1, H), device="cuda", generator=g).to(torch.bfloat16)
+    bufs = {n: torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
+            for n, N in (("qkv", 6144), ("o", H), ("h", F), ("y", H))}
+    st = timer.stream
+    # copy c, linear j at [4 c + j]; absent linears repeat gate/up (never read)
+    flat = [ws[n][c] if n in ws else ws["gate_up"][c] for c in range(copies) for n in LLAMA3_LINEARS]
+    qwa, sca, qza = (ptr_array([t[i] for t in flat]) for i in range(3))
+    loop = make_loop("snxb_loop_decode", C.c_int(copies), C.c_int(1 if layer else 0), x, qwa, sca, qza,
+                     bufs["qkv"], bufs["o"], bufs["h"], bufs["y"], H, 6144, F, C.c_void_p(st))
+
+    def step(c):
+        calls = []
+        gu = ws["gate_up"][c]
+        if layer:
+            q, o, d = ws["qkv"][c], ws["o"][c], ws["down"][c]
+            calls.append(bound(lib, "SNEPPX_qlinear_w4a16", x, q[0], q[1], q[2], None, 0, None, bufs["qkv"],
+                               SNEPPX_BFLOAT16, 1, 6144, H, 128, C.c_void_p(st)))
+            calls.append(bound(lib, "SNEPPX_qlinear_w4a16", bufs["qkv"], o[0], o[1], o[2], None, 0, None,
+                               bufs["o"], SNEPPX_BFLOAT16, 1, H, H, 128, C.c_void_p(st)))
+        calls.append(bound(lib, "SNEPPX_qlinear_w4a16_swiglu", bufs["o"] if layer else x, gu[0], gu[1], gu[2],
+                           None, bufs["h"], 1, F, H, 128, C.c_void_p(st)))
+        if layer:
+            calls.append(bound(lib, "SNEPPX_qlinear_w4a16", bufs["h"], d[0], d[1], d[2], None, 0, None,
+                               bufs["y"], SNEPPX_BFLOAT16, 1, H, F, 128, C.c_void_p(st)))
+        return lambda: [f() for f in calls]
+    total, mean_step, _ = timer.run([step(c) for c in range(copies)], steps, warmup, loop)
+    nbytes = sum(w4_bytes(1, N, K, K // 128) for n, (N, K) in LLAMA3_LINEARS.items() if n in names)
+    nbytes -= 2 * F if "gate_up" in names else 0        # gate/up writes F outputs, not 2 F
+    host = {n: tuple(t.cpu() for t in ws[n][0]) for n in names}
+    return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
+            "host": {"w": host, "x": _u16(x)}}
 
 
 def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
@@ -439,6 +488,13 @@ def _u16(t):
     return t.cpu().view(torch.int16).numpy().view(np.uint16)
 
 
+def _bf16_np(a):
+    """float32 -> bf16 bits, round to nearest even (the GPU's output rounding)."""
+    import numpy as np
+    b = np.ascontiguousarray(a, np.float32).view(np.uint32)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+
+
 def _per_call(fn, seconds, max_reps=200):
     """Seconds per call of fn(), repeated for about `seconds` (at least once)."""
     reps, t0 = 0, time.perf_counter()
@@ -490,6 +546,27 @@ def cpu_legs(orc, jobs, seconds):
                                                f"{A.shape[0]} of {M} rows of A against all of W, "
                                                f"{per:.2f} s per slice, extrapolated linearly to M={M} "
                                                f"({full:.0f} s per call)")
+        elif kind == "decode":                 # C5 linears at M = 1, full shapes
+            w = {n: (v[0].numpy().view(np.uint32), v[1].numpy().view(np.uint16), v[2].numpy().view(np.uint32))
+                 for n, v in h["w"].items()}
+
+            def token():
+                xs = h["x"]
+                if h["layer"]:
+                    rc, q = orc.w4a16_linear(xs, *w["qkv"], None, 6144, 4096, 128)
+                    xs = _bf16_np(q[:, :4096])
+                    rc, o = orc.w4a16_linear(xs, *w["o"], None, 4096, 4096, 128)
+                    xs = _bf16_np(o)
+                rc, gu = orc.w4a16_linear(xs, *w["gate_up"], None, 28672, 4096, 128)
+                g = gu[:, :14336]
+                with np.errstate(over="ignore"):
+                    act = _bf16_np((g / (np.float32(1) + np.exp(-g)) * gu[:, 14336:]).astype(np.float32))
+                if h["layer"]:
+                    orc.w4a16_linear(act, *w["down"], None, 4096, 14336, 128)
+            per, reps, el = _per_call(token, seconds, max_reps=20)
+            entry["cpu_baseline"] = _cpu_entry(round(h["bytes"] / per / 1e9, 4), "GB/s",
+                                               f"full shapes M=1, {reps} calls in {el:.1f} s "
+                                               f"({per * 1e3:.1f} ms/call)")
         elif kind == "chain":                  # C5: token slices, extrapolated to T
             shapes, w = h["shapes"], h["w"]
 
@@ -588,6 +665,11 @@ def run_only(args, lib, timer, torch, N, K, group):
         st = timer.stream
         t, _, _ = timer.run([lambda: lib.qlinear_w4a16(x, qw, sc, qz, None, K2 // 128, y, 128, stream=st)], steps, 2)
         print(f"gemm-w4 T={T} N={N2} K={K2}: {t / steps * 1e3:.1f} us, {2 * T * N2 * K2 / (t / steps) / 1e9:.0f} TFLOP/s")
+    elif args.only == "decode":
+        for layer in (False, True):
+            r = bench_decode(lib, timer, torch, 4 if layer else 8, steps, args.warmup, layer)
+            print(f"decode {'layer' if layer else 'gate/up+swiglu'}: {r['ms_per_step'] * 1e3:.2f} us, "
+                  f"{r['gbs']:.0f} GB/s ({r['gbs'] / HBM_PEAK_GBS:.3f})")
     elif args.only == "mx":
         for fmt in MX_BENCH:
             r = bench_mx(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fmt)
@@ -658,6 +740,17 @@ def main():
                           "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
                           "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5)})
             cpu_jobs.append((extra[-1], "w4_gidx", dict(r["host"], bytes=r["bytes"])))
+        for layer in (False, True):
+            r = bench_decode(lib, timer, torch, 4 if layer else 8, max(50, args.steps // 4), 10, layer)
+            what = ("Llama-3-8B layer linears at decode (QKV, O, gate/up + SwiGLU fused, down; "
+                    "4 launches, attention and norms excluded)" if layer else
+                    "Llama-3-8B gate/up projection + SwiGLU fused, one launch (F=14336, K=4096)")
+            extra.append({"workload": f"{what} W4A16 g128 M=1", "value": round(r["gbs"], 1), "unit": "GB/s",
+                          "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "bytes": r["bytes"],
+                          "ms_per_step": round(r["ms_per_step"], 5)})
+            cpu_jobs.append((extra[-1], "decode", dict(r["host"], bytes=r["bytes"], layer=layer)))
+            print(f"[bench] {what}: {r['gbs']:.0f} GB/s, {r['ms_per_step'] * 1e3:.2f} us",
+                  file=sys.stderr, flush=True)
         r = bench_w8(lib, timer, torch, 4096, 4096, 20, max(50, args.steps // 4), 10)
         extra.append({"workload": "C1 W8 weight-only GEMV N=4096 K=4096 M=1 fp32", "value": round(r["gbs"], 1),
                       "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),

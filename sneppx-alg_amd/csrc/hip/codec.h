@@ -131,4 +131,12 @@ __device__ __forceinline__ uint16_t bf16_out(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+// SiLU(g) * u as the fused SwiGLU epilogue computes it: the exponential and
+// the reciprocal on the hardware's fast approximations (about 1 ulp each,
+// far below the bf16 rounding of the result).  Large negative g gives
+// exp = inf, rcp = 0 and a zero product; NaN propagates.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+    return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+}
+
 }  // namespace snx

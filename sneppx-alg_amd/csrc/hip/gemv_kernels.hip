@@ -547,7 +547,11 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
 // returns its loads in issue order; the weight loads are nontemporal.
 // PERM: the columns of qw are stored in the order perm (uint16 [K]), so the
 // activations are gathered x[perm[k']] from LDS before staging.
-template <int T, bool ZEROS, bool YF32, bool PERM>
+// GLU: qw / scales / qzeros hold a stacked gate/up projection [2N][K] (gate
+// rows first) and y is bf16 [N] = silu(gate) * up: wave w of a workgroup
+// owning output rows [wg0, rend) (at most 8) computes gate row n = wg0 + w and
+// up row N + n as its two rows, and lane 63 applies the SwiGLU rule.
+template <int T, bool ZEROS, bool YF32, bool PERM, bool GLU = false>
 __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ qw,
                                                      const uint16_t* __restrict__ scales,
@@ -576,7 +580,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     const int b = blockIdx.x;
     const int wg0 = b * rows_q + (b < rows_rem ? b : rows_rem);
     const int rend = wg0 + rows_q + (b < rows_rem ? 1 : 0);
-    const int n0 = wg0 + wave * RW;
+    const int n0 = GLU ? wg0 + wave : wg0 + wave * RW;
 
     // 1. activations (and perm), then the raw scales / zero words of the 16 rows
     u32x4 xr[XPT], pr[PERM ? XPT : 1];
@@ -591,16 +595,16 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     uint32_t zv = 0u;
     const bool sload = tid < WROWS * SPR;
     const bool zload = ZEROS && tid >= WROWS * SPR && tid < WROWS * (SPR + ZPR);
-    if (sload) {
-        int row = wg0 + tid / SPR;
+    // staged row j = 2 wave + r: row n0 + r, or (GLU) gate / up row of n0
+    auto staged_row = [&](int j) {
+        int row = GLU ? wg0 + (j >> 1) : wg0 + j;
         row = row < rend ? row : rend - 1;
-        sv = load16(scales + (size_t)row * G + (tid % SPR) * 8);
-    }
+        return GLU && (j & 1) ? row + N : row;
+    };
+    if (sload) sv = load16(scales + (size_t)staged_row(tid / SPR) * G + (tid % SPR) * 8);
     if (zload) {
         const int j = tid - WROWS * SPR;
-        int row = wg0 + j / ZPR;
-        row = row < rend ? row : rend - 1;
-        zv = qz[(size_t)row * ZPR + j % ZPR];
+        zv = qz[(size_t)staged_row(j / ZPR) * ZPR + j % ZPR];
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -609,16 +613,16 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     // 2. weights: RW rows x T chunks, all in flight (nontemporal).  A row past
     // the workgroup's share reads zeros without a memory access: its offset
     // lies beyond the buffer's record count.
-    const __amdgpu_buffer_rsrc_t rq =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(qw), (short)0, N * KW * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(qw), (short)0, (GLU ? 2 : 1) * N * KW * 4, 0x00020000);
     u32x4 wv[RW][T];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        const bool live = n0 + r < rend;
+        const bool live = GLU ? n0 < rend : n0 + r < rend;
+        const uint32_t wrow = GLU ? (uint32_t)(n0 + r * N) : (uint32_t)(n0 + r);
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const uint32_t off = live ? (uint32_t)(n0 + r) * (KW * 4) + (uint32_t)(64 * t + lane) * 16u
-                                      : kNoRecord;
+            const uint32_t off = live ? wrow * (KW * 4) + (uint32_t)(64 * t + lane) * 16u : kNoRecord;
             wv[r][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, kNontemporal));
         }
     }
@@ -743,7 +747,13 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         const float d = dg == 0 ? y4[r][0] : dg == 1 ? y4[r][1] : dg == 2 ? y4[r][2] : y4[r][3];
         out[r] = dpp_sum_to_lane63(d - corr[r]);
     }
-    if (lane == 63) {
+    if (lane == 63 && GLU) {
+        if (n0 < rend) {
+            const float g = bias ? out[0] + bias[n0] : out[0];
+            const float u = bias ? out[1] + bias[N + n0] : out[1];
+            reinterpret_cast<uint16_t*>(y)[n0] = bf16_out(silu_mul_fast(g, u));
+        }
+    } else if (lane == 63) {
 #pragma unroll
         for (int r = 0; r < RW; r++) {
             if (n0 + r >= rend) break;
@@ -943,12 +953,13 @@ size_t gemv1_lds(size_t K, bool perm) {
     return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
 }
 
-// Workgroups of the M = 1 kernel: enough for at most 16 rows each, rounded up
-// to a multiple of the CU count once there is more than one per CU, so each
-// workgroup takes an even share of the rows and every CU the same number.
-unsigned gemv1_grid(int N) {
+// Workgroups of the M = 1 kernel: enough for at most `per` rows each (16, or
+// 8 output rows of the GLU form), rounded up to a multiple of the CU count
+// once there is more than one per CU, so each workgroup takes an even share
+// of the rows and every CU the same number.
+unsigned gemv1_grid(int N, int per = 16) {
     const int ncu = snx::cu_count();
-    int nwg = (N + 15) / 16;
+    int nwg = (N + per - 1) / per;
     if (nwg > ncu) nwg = (nwg + ncu - 1) / ncu * ncu;
     return (unsigned)(nwg < N ? nwg : N);
 }
@@ -1002,6 +1013,19 @@ int launch_gemv1(const W4Launch& a) {
         case 7: return launch_gemv1_t<7, PERM>(a);
         default: return launch_gemv1_t<8, PERM>(a);
     }
+}
+
+template <int T>
+int launch_gemv1_glu_t(const W4Launch& a) {
+    dim3 grid(gemv1_grid(a.N, 8)), block(512);
+    const size_t lds = gemv1_lds((size_t)a.K, false);
+#define SNX_G1(Z)                                                                                 \
+    k_w4a16_gemv1<T, Z, false, false, true><<<grid, block, lds, a.s>>>(                           \
+        a.x, a.qw, a.scales, a.qz, nullptr, a.y, a.bias, a.N, a.N / (int)grid.x, a.N % (int)grid.x)
+    if (a.qz) SNX_G1(true);
+    else SNX_G1(false);
+#undef SNX_G1
+    return snx_launch_check("k_w4a16_gemv1<glu>");
 }
 
 template <int XPT, bool PERM>
@@ -1495,6 +1519,35 @@ int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
     return M >= 1 && M <= 4 && K % 512 == 0 && group >= 128 && (group & (group - 1)) == 0 &&
            K % (size_t)group == 0 && snx_w4a16_small_lds(M, K, perm) <= 65536 &&
            M * (K / 8) <= 8 * 256;
+}
+
+// The GLU form of the M = 1 kernel applies: its shapes, with the stacked
+// [2F][K] weights within the buffer offsets.
+int snx_w4a16_gemv1_swiglu_ok(size_t F, size_t K, int group, const void* scales, const void* qzeros) {
+    return F && snx_w4a16_gemv1_ok(1, K, group, scales, qzeros) && (uint64_t)F * K < kNoRecord;
+}
+
+// M = 1 gate/up projection with the SwiGLU step (the GLU form of the M = 1
+// kernel): x bf16 [K], stacked weights [2F][K], out bf16 [F].
+int snx_k_w4a16_gemv1_swiglu(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                             const uint32_t* qzeros, const float* bias, uint16_t* out, size_t F,
+                             size_t K, int group, void* st) {
+    if (!snx_w4a16_gemv1_swiglu_ok(F, K, group, scales, qzeros)) {
+        snx_set_error("w4a16 swiglu gemv: F=%zu K=%zu group %d is not an M = 1 kernel shape", F, K, group);
+        return -1;
+    }
+    W4Launch a{x, qw, scales, qzeros, nullptr, out, bias, 0, 1, (int)F, (int)K, (int)(K / 128), group,
+               0, S(st)};
+    switch (K / 2048) {
+        case 1: return launch_gemv1_glu_t<1>(a);
+        case 2: return launch_gemv1_glu_t<2>(a);
+        case 3: return launch_gemv1_glu_t<3>(a);
+        case 4: return launch_gemv1_glu_t<4>(a);
+        case 5: return launch_gemv1_glu_t<5>(a);
+        case 6: return launch_gemv1_glu_t<6>(a);
+        case 7: return launch_gemv1_glu_t<7>(a);
+        default: return launch_gemv1_glu_t<8>(a);
+    }
 }
 
 int snx_k_w4a16_gemv(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,

@@ -110,14 +110,6 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // each weight column in lanes with h = l / 32, so a lane's eight words for the
 // step are 32 contiguous bytes; the prep pass stores the activations to match
 // (chunk 2 s + h of a prepared row = original columns of word 8 h + s).
-// SiLU(g) * u as the fused SwiGLU epilogue computes it: the exponential and
-// the reciprocal on the hardware's fast approximations (about 1 ulp each,
-// far below the bf16 rounding of the result).  Large negative g gives
-// exp = inf, rcp = 0 and a zero product; NaN propagates.
-__device__ __forceinline__ float silu_mul_fast(float g, float u) {
-    return g * u * __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-}
-
 // SWIGLU: the weights are a stacked [2F][K] gate/up projection and the output
 // is [M][F] = bf16(silu(gate) * up) (N = F).  Tile column c < 128 is gate
 // column n0 + c, column c >= 128 the up column F + n0 + c - 128 of the same

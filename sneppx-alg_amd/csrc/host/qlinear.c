@@ -300,7 +300,11 @@ int SNEPPX_qlinear_w4a16_swiglu(const uint16_t* x, const uint32_t* qweight,
                                               group, Mp, stream);
         return rc;
     }
-    /* decode rows: the [M][2F] projection in fp32 scratch, then the same rule */
+    /* one decode row: gate and up rows of an output in one wave, SwiGLU on its total */
+    if (M == 1 && aligned16(x) && aligned16(qweight) &&
+        snx_w4a16_gemv1_swiglu_ok(F, K, group, scales, qzeros))
+        return snx_k_w4a16_gemv1_swiglu(x, qweight, scales, qzeros, bias, out, F, K, group, stream);
+    /* other decode rows: the [M][2F] projection in fp32 scratch, then the same rule */
     float* gu = (float*)snx_workspace(M * 2 * F * sizeof(float), 0, stream);
     if (!gu) return -1;
     int rc = SNEPPX_qlinear_w4a16(x, qweight, scales, qzeros, NULL, 0, bias, gu, SNEPPX_FLOAT32, M,

@@ -130,6 +130,10 @@ int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm);
 /* the M = 1 streaming decode kernel applies (group 128, K = 2048 T <= 16384,
  * scales 16-byte and qzeros 4-byte aligned); perm may be given */
 int snx_w4a16_gemv1_ok(size_t M, size_t K, int group, const void* scales, const void* qzeros);
+int snx_w4a16_gemv1_swiglu_ok(size_t F, size_t K, int group, const void* scales, const void* qzeros);
+int snx_k_w4a16_gemv1_swiglu(const uint16_t* x, const uint32_t* qw, const uint16_t* scales,
+                             const uint32_t* qzeros, const float* bias, uint16_t* out, size_t F,
+                             size_t K, int group, void* st);
 /* split-K decode (5 <= M <= 16): K span per workgroup (0 = unsupported),
  * partials part [K/kspan][M][N] fp32, then the ordered reduction */
 int snx_w4a16_splitk_span(size_t M, size_t K, int group);

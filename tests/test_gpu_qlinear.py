@@ -662,7 +662,12 @@ def test_w8_gemv_activations_far_from_zero_mean(lib, oracle, K, mean):
     (256, 512, 4096, True, True),       # one M tile, symmetric, bias
     (600, 14336, 4096, False, False),   # the Llama MLP width (sampled rows)
     (4, 1000, 4096, False, True),       # decode rows: fp32 projection, then the same rule
-    (1, 512, 2048, True, False),
+    (1, 512, 2048, True, False),        # one row: gate and up rows in one wave of the M = 1 kernel
+    (1, 14336, 4096, False, True),      # the Llama-3-8B MLP width at decode
+    (1, 11008, 4096, False, False),
+    (1, 1000, 4096, False, True),       # ragged row shares
+    (1, 3000, 14336, False, True),      # K = 14336
+    (1, 24, 2048, True, True),          # fewer workgroups than CUs, short shares
 ])
 def test_w4a16_swiglu(lib, oracle, M, F, K, sym, bias):
     """out = bf16(silu(g) * u), g / u the gate / up halves of the stacked
