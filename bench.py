@@ -365,8 +365,12 @@ def bench_mx(lib, timer, torch, M, N, K, steps, warmup, fmt="mxfp4_e2m1", mfma_f
         call = lambda: lib.qlinear_mx_gemm(pa, sa, pw, sw, fmt, out, M, N, K, stream=st, mfma_form=mfma_form)
     total, mean_launch, _ = timer.run([call], steps, warmup)
     flops = 2 * M * N * K
+    rb = pa.shape[1] if pa.dim() == 2 else pa.numel() // M          # code bytes per row
+    host = {"pa": pa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(), "sa": sa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(),
+            "pw": pw.reshape(N, -1).cpu().numpy(), "sw": sw.reshape(N, -1).cpu().numpy(),
+            "M": M, "N": N, "K": K, "fmt": fmt, "flops": flops, "row_bytes": rb}
     return {"ms_per_step": total / steps, "tflops": flops / (total / steps) / 1e9,
-            "tflops_kernel": flops / mean_launch / 1e9}
+            "tflops_kernel": flops / mean_launch / 1e9, "host": host}
 
 
 def bench_vendor_w8a8(torch, M, N, K, steps, warmup):
@@ -567,6 +571,27 @@ def cpu_legs(orc, jobs, seconds):
             entry["cpu_baseline"] = _cpu_entry(round(h["bytes"] / per / 1e9, 4), "GB/s",
                                                f"full shapes M=1, {reps} calls in {el:.1f} s "
                                                f"({per * 1e3:.1f} ms/call)")
+        elif kind == "mx":                     # MX GEMM: decode W once, rows of A extrapolated
+            sys.path.insert(0, os.path.join(REPO, "oracle"))
+            import mx_oracle
+            from threadpoolctl import threadpool_limits
+            M, N, K, fmt, r = h["M"], h["N"], h["K"], h["fmt"], h["pa"].shape[0]
+            nw = min(N, 512)                   # rows of W decoded (the numpy bit unpack is slow)
+            with threadpool_limits(limits=1):
+                t0 = time.perf_counter()
+                wd = mx_oracle.dequantize(h["pw"][:nw].reshape(-1), h["sw"][:nw].reshape(-1), (nw, K),
+                                          fmt).astype(np.float32)
+                t_w = time.perf_counter() - t0
+                t0 = time.perf_counter()
+                ad = mx_oracle.dequantize(h["pa"].reshape(-1), h["sa"].reshape(-1), (r, K), fmt).astype(np.float32)
+                ad @ wd.T
+                t_rows = time.perf_counter() - t0
+            full = (t_w + t_rows * M / r) * N / nw
+            entry["cpu_baseline"] = _cpu_entry(round(h["flops"] / full / 1e12, 6), "TFLOP/s",
+                                               f"numpy oracle dequantize of {nw} rows of W ({t_w:.1f} s) + {r} rows "
+                                               f"of A dequantized and multiplied with them in fp32 ({t_rows:.2f} s), "
+                                               f"extrapolated linearly to M={M}, N={N} ({full:.0f} s per call)")
+            entry["cpu_baseline"]["build"] = "oracle/mx_oracle.py (numpy), BLAS limited to one thread"
         elif kind == "chain":                  # C5: token slices, extrapolated to T
             shapes, w = h["shapes"], h["w"]
 
@@ -791,6 +816,8 @@ def main():
                               "frac_of_peak": round(r["tflops"] / peak, 4),
                               "ms_per_step": round(r["ms_per_step"], 4)})
                 print(f"[bench] {extra[-1]['workload']}: {r['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
+                if not kept:
+                    cpu_jobs.append((extra[-1], "mx", r["host"]))
 
     cpu = None
     if not args.no_cpu:
