@@ -149,13 +149,14 @@ def test_qlayer_bias_forward_and_file_round_trip(lib, oracle, tmp_path, fmt, M):
     np.testing.assert_array_equal(layer.matmul_host(x), y0)
 
 
-def test_matmul_host_is_reentrant(lib):
+@pytest.mark.parametrize("fmt", ["w4", "w8"])
+def test_matmul_host_is_reentrant(lib, fmt):
     """SNEPPX_qlayer_matmul_host replaces the reentrant matmul_3d
     (attention.c:324-346): two host threads calling it at once on one layer,
     with different row counts and inputs, get the single-threaded results."""
     import threading
     K, N = 2048, 1000
-    layer = lib.qlayer_create_kn(np.random.default_rng(1).normal(0, 0.02, (K, N)).astype(np.float32), "w4", 128)
+    layer = lib.qlayer_create_kn(np.random.default_rng(1).normal(0, 0.02, (K, N)).astype(np.float32), fmt, 128)
     xs = [np.random.default_rng(10 + t).normal(0, 1, (m, K)).astype(np.float32) for t, m in enumerate((3, 37))]
     want = [layer.matmul_host(x) for x in xs]
     errors = []

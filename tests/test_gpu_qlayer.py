@@ -151,30 +151,3 @@ def test_create_rejects_bad_arguments(lib):
     with pytest.raises(Exception, match="group"):
         lib.qlayer_create_kn(_weights(128, 8, 0), "w4", 12)     # not a multiple of 8
 
-
-@pytest.mark.parametrize("fmt", ["w4", "w8"])
-def test_matmul_host_from_two_threads(lib, fmt):
-    """The host drop-in is reentrant like the reference's matmul_3d
-    (attention.c:324-346): two threads calling one layer at once, with
-    different inputs and row counts, each get the serial answer every time."""
-    import threading
-    print(f"[gpu] qlayer matmul_host two threads {fmt}", flush=True)
-    K, N = 2048, 1536
-    layer = lib.qlayer_create_kn(_weights(K, N, 21), fmt, 128)
-    xs = [np.random.default_rng(s).normal(0, 1, (m, K)).astype(np.float32) for s, m in ((1, 3), (2, 64))]
-    want = [layer.matmul_host(x) for x in xs]
-    bad = []
-
-    def run(i):
-        for _ in range(25):
-            y = layer.matmul_host(xs[i])
-            if not np.array_equal(y, want[i]):
-                bad.append(i)
-                return
-
-    th = [threading.Thread(target=run, args=(i,)) for i in range(2)]
-    for t in th:
-        t.start()
-    for t in th:
-        t.join()
-    assert not bad
