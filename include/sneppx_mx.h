@@ -88,7 +88,10 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
  * exponent field (E4M3 0x7F = 480, E5M2 65536 .. 114688) are not, so MXFP8
  * operands first pass through SNEPPX_mx_to_mfma into the calling thread's
  * workspace (one read and write of A and W per call).  MXFP8/6: K % 128 == 0,
- * exponents 4-byte aligned; MXFP4 as SNEPPX_qlinear_mxfp4_gemm. */
+ * exponents 4-byte aligned; MXFP4 as SNEPPX_qlinear_mxfp4_gemm.  In every MX
+ * GEMM an exponent of -128 (the reference's int8 cast gives it to blocks
+ * whose peak lies near 2^-128 times the format's largest element) is taken
+ * as -127: the matrix cores' E8M0 scale has no 2^-128. */
 int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                            SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype, size_t M,
                            size_t N, size_t K, SNEPPXStream stream);
