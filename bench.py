@@ -96,6 +96,7 @@ class Timer:
             self.lib.record(evs[i][1], self.stream)
         torch.cuda.synchronize()
         per = sorted(self.lib.elapsed_ms(s, e) for s, e in evs)
+        self.pcts = (per[len(per) // 10], per[(9 * len(per)) // 10])     # p10, p90 of the last run
         for s, e in evs:
             self.lib.fn["snx_hip_event_destroy"](s)
             self.lib.fn["snx_hip_event_destroy"](e)
@@ -713,6 +714,20 @@ def run_only(args, lib, timer, torch, N, K, group):
         print(f"copy: {steps} x {n} bytes")
 
 
+def _gpu_sclk_mhz():
+    """Current shader clock of the first GPU from sysfs (the line marked '*'
+    of pp_dpm_sclk), or None where the file is absent or unreadable."""
+    import glob
+    for path in sorted(glob.glob("/sys/class/drm/card*/device/pp_dpm_sclk")):
+        try:
+            for line in open(path):
+                if line.rstrip().endswith("*"):
+                    return int("".join(ch for ch in line.split(":", 1)[1] if ch.isdigit()))
+        except (OSError, ValueError, IndexError):
+            continue
+    return None
+
+
 def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -744,6 +759,7 @@ def main():
         run_only(args, lib, timer, torch, N, K, group)
         return
     head, keep = bench_w4a16(lib, timer, torch, M, N, K, group, args.copies, args.steps, args.warmup)
+    head_pcts, head_sclk = timer.pcts, _gpu_sclk_mhz()
     print(f"[bench] C2 M=1: {head['gbs']:.0f} GB/s whole-job, kernel {head['launch_ms_mean'] * 1e3:.2f} us",
           file=sys.stderr, flush=True)
 
@@ -853,12 +869,15 @@ def main():
         "data": "synthetic (seeded torch.randn N(0,0.02) weights quantized on the GPU, N(0,1) bf16 activations)",
         "config": {"workload": "C2 W4A16 AWQ-style g128 decode GEMV", "N": N, "K": K, "M": M,
                    "group": group, "weight_copies": args.copies,
-                   "bytes_per_step": head["bytes"], "device": arch, "cus": cus},
+                   "bytes_per_step": head["bytes"], "device": arch, "cus": cus,
+                   "seeds": {"weights": 2, "activations": 3}, "gpu_clock_max_mhz": clk // 1000,
+                   "gpu_sclk_mhz_after_run": head_sclk},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "k_w4a16_gemv1", "algorithmic_bytes": head["bytes"],
                      "launch_us": round(head["ms_per_step"] * 1e3, 3),
-                     "event_pair_us_median": round(head["launch_ms_median"] * 1e3, 3)},
+                     "event_pair_us_median": round(head["launch_ms_median"] * 1e3, 3),
+                     "event_pair_us_p10_p90": [round(head_pcts[0] * 1e3, 3), round(head_pcts[1] * 1e3, 3)]},
         "cpu_baseline": cpu,
         "extra": extra,
     }
