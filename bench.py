@@ -640,6 +640,27 @@ def cpu_baseline(ws_host, x_host, N, K, group, seconds):
             break
     per = el / reps
     nbytes = w4_bytes(1, N, K, K // group)
+    # the same restatement on every host thread, rows split evenly (a labelled
+    # second figure; the reference path itself is single-threaded)
+    import threading
+    nth = max(1, min(16, os.cpu_count() or 1))
+    bounds = [N * i // nth for i in range(nth + 1)]
+
+    def part(i):
+        lo, hi = bounds[i], bounds[i + 1]
+        orc.w4a16_linear(x_host, qw[lo:hi], sc[lo:hi], qz[lo:hi], None, hi - lo, K, group)
+
+    treps, t0 = 0, time.perf_counter()
+    while True:
+        ths = [threading.Thread(target=part, args=(i,)) for i in range(nth)]
+        for t in ths:
+            t.start()
+        for t in ths:
+            t.join()
+        treps += 1
+        tel = time.perf_counter() - t0
+        if tel >= seconds / 3 or treps >= 200:
+            break
     w = np.random.default_rng(11).normal(0, 0.02, (4096, 4096)).astype(np.float32)
     t1 = time.perf_counter()
     for _ in range(3):
@@ -649,6 +670,9 @@ def cpu_baseline(ws_host, x_host, N, K, group, seconds):
             "sample": f"full C2 shape N={N} K={K} M=1, {reps} calls in {el:.1f} s "
                       f"({per * 1e3:.1f} ms/call), oracle/liboracle_perf.so (-O3 -march=x86-64-v3)",
             "quantize_int8_channel_4096x4096_ms": round(q_ms, 2),
+            "restatement_threads": {"value": round(nbytes / (tel / treps) / 1e9, 3), "unit": "GB/s",
+                                    "cores": nth, "sample": f"rows split over {nth} host threads, "
+                                                            f"{treps} calls in {tel:.1f} s"},
             "host_cpu": _cpu_name(), "host_threads_available": os.cpu_count()}
 
 
