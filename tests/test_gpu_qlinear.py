@@ -715,3 +715,36 @@ def test_w4a16_subnormal_fp16_scales(lib, oracle, M, K, group):
     got = y.cpu().numpy()
     assert np.abs(yo[:, ::3]).max() < 1e-3 * np.abs(yo[:, 1::3]).max()
     assert rel_err(got[:, ::3], yo[:, ::3]) <= TOL_F32
+
+
+def test_decode_token_through_llama3_layer_linears(lib, oracle):
+    """One token (M = 1) through the four linears of a Llama-3-8B layer as the
+    bench's decode line runs them (QKV 6144x4096, O 4096x4096 on the first
+    4096 QKV outputs, gate/up + SwiGLU 2x14336x4096 in one launch, down
+    4096x14336), each stage against the oracle fed the same bf16 input."""
+    print("[gpu] decode token through the Llama-3-8B layer linears", flush=True)
+    H, F = 4096, 14336
+    rng = np.random.default_rng(77)
+    w = {n: _w4_case(oracle, N, K, 128, 80 + i)
+         for i, (n, N, K) in enumerate((("qkv", 6144, H), ("o", H, H), ("gu", 2 * F, H), ("down", H, F)))}
+    x = bf16_bits(rng.normal(0, 1, (1, H)).astype(np.float32))
+    dev = {n: tuple(to_dev(a) for a in v[:3]) for n, v in w.items()}
+    qkv = torch.empty((1, 6144), dtype=torch.bfloat16, device=DEV)
+    o = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
+    h = torch.empty((1, F), dtype=torch.bfloat16, device=DEV)
+    y = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), *dev["qkv"], None, H // 128, qkv, 128)
+    lib.qlinear_w4a16(qkv[:, :H], *dev["o"], None, H // 128, o, 128)       # the first 4096 values
+    lib.qlinear_w4a16_swiglu(o, *dev["gu"], h, 128)
+    lib.qlinear_w4a16(h, *dev["down"], None, F // 128, y, 128)
+    torch.cuda.synchronize()
+    # each stage against the oracle on the GPU's own (bf16) input to it
+    steps = (("qkv", x, qkv, 6144, H), ("o", u16(qkv)[:, :H], o, H, H), ("down", u16(h), y, H, F))
+    for name, inp, got, N, K in steps:
+        qw, sc, qz, _ = w[name]
+        rc, want = oracle.w4a16_linear(np.ascontiguousarray(inp), qw, sc, qz, None, N, K, 128)
+        assert rel_err(bf16_to_f32(u16(got)), want) <= TOL_BF16, name
+    qw, sc, qz, _ = w["gu"]
+    rc, gu = oracle.w4a16_linear(u16(o), qw, sc, qz, None, 2 * F, H, 128)
+    g, u = gu[:, :F].astype(np.float64), gu[:, F:].astype(np.float64)
+    assert rel_err(bf16_to_f32(u16(h)), g / (1.0 + np.exp(-g)) * u) <= TOL_BF16
