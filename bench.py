@@ -31,6 +31,11 @@ FP8_PEAK_TOPS = 5033.2         # dense fp8 MFMA
 BF16_PEAK_TFLOPS = 2516.6      # dense bf16 MFMA
 FP4_PEAK_TFLOPS = 10066.3      # dense fp4 MFMA (MXFP4)
 FP6_PEAK_TFLOPS = 10066.3      # dense fp6 MFMA (MXFP6)
+# MFMA-heavy kernels reach their steady shader clock only after ~30 ms of
+# work: C4 fp8 measured 2278 TOPS timed after 30 warm-up launches and
+# 2527-2553 TOPS after 300-3000 (one box, 200 timed launches each), so the
+# GEMM lines warm up for 300 launches (~30 ms) before their timed launches.
+GEMM_WARMUP, GEMM_STEPS = 300, 200
 MX_BENCH = {"mxfp4_e2m1": FP4_PEAK_TFLOPS, "mxfp8_e4m3": FP8_PEAK_TOPS, "mxfp8_e5m2": FP8_PEAK_TOPS,
             "mxfp6_e3m2": FP6_PEAK_TFLOPS, "mxfp6_e2m3": FP6_PEAK_TFLOPS}
 SNEPPX_BFLOAT16 = 3            # SNEPPXDtype of include/sneppx_qlinear.h
@@ -401,7 +406,8 @@ def bench_vendor_w8a8(torch, M, N, K, steps, warmup):
             torch.cuda.synchronize()
             ms = e0.elapsed_time(e1) / steps
             out.append({"workload": f"vendor reference (hipBLASLt, not this library): {name} M={M} N={N} K={K}",
-                        "value": round(2 * M * N * K / ms / 1e9, 1), "unit": "TOPS", "ms_per_step": round(ms, 4)})
+                        "value": round(2 * M * N * K / ms / 1e9, 1), "unit": "TOPS", "ms_per_step": round(ms, 4),
+                        "steps": steps, "warmup": warmup})
         except Exception as e:   # a torch build without the op: report, do not fail the bench
             out.append({"workload": f"vendor reference: {name}", "value": None, "error": str(e)[:120]})
     del a, w, af, wf
@@ -826,35 +832,37 @@ def main():
         extra.append({"workload": "host API SNEPPX_quantize_int8_channel 4096x4096 (host buffers, PCIe included)",
                       "value": round(h["ms_per_call"], 3), "unit": "ms", "higher_is_better": False,
                       "gbs_pcie_inclusive": round(h["gbs_pcie_inclusive"], 2)})
-        r = bench_chain(lib, timer, torch, 10, 5)
+        r = bench_chain(lib, timer, torch, 10, 30)
         extra.append({"workload": f"C5 Llama-3-8B layer W4A16 g128 linear chain T={r['T']} "
                                   f"(16 decode + 8 prefill chunks {r['chunk_lens']})",
                       "value": round(r["tflops"], 1), "unit": "TFLOP/s",
                       "frac_of_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
-                      "ms_per_step": round(r["ms_per_step"], 4), "per_linear": r["per_linear"]})
+                      "ms_per_step": round(r["ms_per_step"], 4), "steps": 10, "warmup": 30,
+                      "per_linear": r["per_linear"]})
         cpu_jobs.append((extra[-1], "chain", dict(r["host"], T=r["T"], flops=r["flops"])))
         print(f"[bench] C5 chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s",
               file=sys.stderr, flush=True)
         for fp8 in (False, True):
-            # MFMA-heavy kernels reach steady clocks only after tens of launches
-            r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, 50, 30, fp8=fp8)
+            r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP, fp8=fp8)
             peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS
             extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N=14336 K=4096",
                           "value": round(r["tops"], 1), "unit": "TOPS",
-                          "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4)})
+                          "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4),
+                          "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
             cpu_jobs.append((extra[-1], "fp8" if fp8 else "i8", r["host"]))
         torch.cuda.synchronize()
-        extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, 50, 30))
+        extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP))
         for fmt, peak in MX_BENCH.items():
             for kept in ((False, True) if fmt.startswith("mxfp8") else (False,)):
-                r = bench_mx(lib, timer, torch, 2048, 14336, 4096, 50, 30, fmt, mfma_form=kept)
+                r = bench_mx(lib, timer, torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP, fmt, mfma_form=kept)
                 how = ("operands kept in matrix-core form" if kept else
                        "both operands converted every call" if fmt.startswith("mxfp8") else
                        "reference MX encoding")
                 extra.append({"workload": f"{fmt.upper()} GEMM M=2048 N=14336 K=4096 ({how}, bf16 out)",
                               "value": round(r["tflops"], 1), "unit": "TFLOP/s",
                               "frac_of_peak": round(r["tflops"] / peak, 4),
-                              "ms_per_step": round(r["ms_per_step"], 4)})
+                              "ms_per_step": round(r["ms_per_step"], 4), "steps": GEMM_STEPS,
+                              "warmup": GEMM_WARMUP})
                 print(f"[bench] {extra[-1]['workload']}: {r['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
                 if not kept:
                     cpu_jobs.append((extra[-1], "mx", r["host"]))
