@@ -811,25 +811,34 @@ __global__ void __launch_bounds__(512) k_gemm_x32(const int8_t* __restrict__ A,
     }
 }
 
-// Persistent int8 GEMM (the C4 int8 kernel).  Same tile, wave layout (8 waves
-// of 32 x 224), LDS ring, swizzle and MFMA as k_gemm_x32, but:
-//  * one workgroup per CU walks tiles b, b + nb, ... (nb = grid size, a
-//    multiple of 8, so every tile of a workgroup stays on its XCD);
-//  * operands go global -> LDS with buffer_load ... lds, counted by vmcnt
-//    only, so the fragment reads of k-step s + 1 stay in flight (lgkmcnt)
-//    across the MFMAs of k-step s instead of draining before each MFMA;
-//  * the last stage of a tile loads the next tile's stage 0 and, after the
-//    stage barrier, its first fragments; the epilogue then stages the bf16
-//    rows through the buffer the last stage freed (two passes of 16 rows per
-//    wave) and writes them with buffer stores (rows/columns outside the
-//    matrix get an out-of-range offset and are dropped), so the output write
-//    of tile i drains while tile i + 1 computes.
-// Barriers are raw s_barrier with explicit waits: a __syncthreads() fence
-// would also wait for the next stage's loads and the previous tile's stores.
 constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every output buffer
 
-template <bool RAW, bool BIAS>
-__global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
+// Persistent form of k_gemm_8w (the C4 kernel for int8 and fp8 e4m3): the
+// same 256 x 224 tile, 4 (M) x 2 (N) waves of 64 x 112 in 16 x 16 MFMA
+// blocks, LDS ring, swizzle and fragment reads, with
+//  * one workgroup per CU walking tiles b, b + nb, ... (nb a multiple of 8:
+//    every tile of a workgroup stays on its XCD);
+//  * each k-step's wait and barrier at its end, after its MFMAs, so the last
+//    k-step of a tile loads the next tile's stage 0 and the next tile starts
+//    computing at once;
+//  * an epilogue that stages each wave's bf16 rows through its own slice of
+//    the buffer the last k-step freed (two passes of 32 rows x 112 columns)
+//    and writes 224-byte row pieces with 16-byte buffer stores (rows or
+//    columns outside the matrix get an out-of-range offset and are dropped),
+//    so tile i's output drains while tile i + 1 computes.  A wave reads back
+//    only what it wrote, so no barrier sits between staging and stores.
+// Requires N % 8 == 0 (a 16-byte piece never straddles a row end), a 16-byte
+// aligned output below 2 GiB and operands below 2 GiB.
+constexpr int PCROW = 120;   // u16 per staged output row of a wave: 112 + 8 pad
+static_assert(8 * 32 * PCROW * 2 <= TLDS_STAGE, "a pass of every wave fits in one stage buffer");
+// A tile's int8 row / column scales and its bias wait in LDS beside the ring
+// (256 floats each, loaded straight from global memory when the tile starts)
+// instead of in registers across the K loop.
+constexpr int PSCALES = 2 * TLDS_STAGE;
+constexpr int PLDS = PSCALES + 3 * 256 * 4;
+
+template <bool FP8, bool RAW, bool BIAS>
+__global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
                                                   const int8_t* __restrict__ W,
                                                   const float* __restrict__ sA,
                                                   const float* __restrict__ sW,
@@ -837,16 +846,16 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
                                                   uint16_t* __restrict__ out,
                                                   const float* __restrict__ bias, int M, int N,
                                                   int K, int tiles_m, int tiles_n) {
-    constexpr int FN = TBN / 32;
+    constexpr int FM = 4;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r32 = lane & 31, h = lane >> 5;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int r16 = lane & 15, q = lane >> 4;
     const int b = blockIdx.x, nb = gridDim.x;
     const int ntiles = tiles_m * tiles_n;
     const int lrow = lane >> 3, lslot = lane & 7;
     auto tile_of = [&](int t) { return (ntiles % 8 == 0) ? (t % 8) * (ntiles / 8) + t / 8 : t; };
-    // per-lane byte offsets of the direct loads (rows clamped into the matrix)
     auto addr = [&](int t, uint32_t* ga, uint32_t* gw) {
         const int tl = tile_of(t);
         const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
@@ -863,6 +872,9 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, N * K, 0x00020000);
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc((void*)out, (short)0, BUF_DROP, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc((void*)sA, (short)0, FP8 ? 4 : M * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsw = __builtin_amdgcn_make_buffer_rsrc((void*)sW, (short)0, FP8 ? 4 : N * 4, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rbi = __builtin_amdgcn_make_buffer_rsrc((void*)bias, (short)0, BIAS ? N * 4 : 0, 0x00020000);
     auto dload = [&](int buf, const uint32_t* ga, const uint32_t* gw, int k0) {
         int8_t* base = lds + buf * TLDS_STAGE;
 #pragma unroll
@@ -874,137 +886,166 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
         if (wave < 4)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr_t)(base + TLDS_A + (24 + wave) * 1024), 16, gw[3], k0, 0, 0);
     };
-    const int sw = swz(r32);
-    const int8_t* arow = lds + (wave * 32 + r32) * TBK;
-    const int8_t* wrow = lds + TLDS_A + r32 * TBK;
+    typedef typename std::conditional<FP8, f32x4, i32x4>::type acc_t;
+    acc_t acc[FM][TFN];
+    const int sw = swz(r16);
+    const int8_t* arow = lds + (wm * 64 + r16) * TBK;
+    const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
     const int nk = K / TBK;
-    i32x16 acc[FN];
-    i32x4 fa[2], fw[2][FN];
-    // fragments of k-step s (chunk 2 s + h) of buffer buf into register slot
-    auto rd = [&](int slot, int buf, int s) {
-        const int off = ((2 * s + h) ^ sw) << 4;
-        fa[slot] = lds16(arow + buf * TLDS_STAGE + off);
+
+    // int8: each k-step is two halves h (the even / odd 16-byte chunks, the
+    // same bank pattern as the fp8 reads; any k order works as long as A and
+    // W agree).  The second half's fragments are read while the first half's
+    // MFMAs run, and the next k-step's first half right after the barrier,
+    // while this k-step's second half runs.
+    i32x4 h0a[FM], h0w[TFN], h1a[FM], h1w[TFN];
+    auto rdh = [&](i32x4* fa, i32x4* fw, int bufi, int h) {
+        const int off = bufi * TLDS_STAGE + (((2 * q + h) ^ sw) << 4);
 #pragma unroll
-        for (int j = 0; j < FN; j++) fw[slot][j] = lds16(wrow + buf * TLDS_STAGE + j * 32 * TBK + off);
-    };
-    auto mm = [&](int slot) {
+        for (int i = 0; i < FM; i++) fa[i] = lds16(arow + off + i * 16 * TBK);
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[slot], fw[slot][j], acc[j], 0, 0, 0);
+        for (int j = 0; j < TFN; j++) fw[j] = lds16(wrow + off + j * 16 * TBK);
     };
-    // issue order inside a k-step: each MFMA followed by two fragment reads
-    // (and, in the first k-step, one direct load of the next stage)
-    auto pattern = [&](bool loads) {
+    auto mmh = [&](const i32x4* fa, const i32x4* fw) {
 #pragma unroll
-        for (int q = 0; q < 7; q++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-            if (q < 4) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-            if (loads) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        }
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < TFN; j++)
+                acc[i][j] = (acc_t)__builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fw[j], (i32x4)acc[i][j], 0, 0, 0);
     };
+
     int t = b;
     if (t >= ntiles) return;
+    const float sa8 = FP8 ? sA[0] : 0.0f, sw8 = FP8 ? sW[0] : 0.0f;   // fp8: per-tensor scales
     uint32_t ga[4], gw[4];
     addr(t, ga, gw);
     dload(0, ga, gw, 0);
     __builtin_amdgcn_s_waitcnt(0x0070);        // vmcnt(0) lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     int buf = 0;
-    rd(0, buf, 0);
+    if (!FP8) rdh(h0a, h0w, 0, 0);
     for (;;) {
         const int tl = tile_of(t);
         const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
         const int tnext = t + nb;
         const bool has_next = tnext < ntiles;
-        float sa[16], swv[FN];
-        if (!RAW) {
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                sa[v] = sA[m < M ? m : M - 1];
+        // this tile's scales / bias into LDS (landed by the first k-step's wait)
+        {
+            const int e = 64 * (wave & 3) + lane;
+            if (!FP8 && !RAW && wave < 4) {
+                const int m = m0 + e < M ? m0 + e : M - 1;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsa, (lds_ptr_t)(lds + PSCALES + 256 * wave), 4,
+                                                         (uint32_t)m * 4u, 0, 0, 0);
             }
-#pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int n = n0 + j * 32 + r32;
-                swv[j] = sW[n < N ? n : N - 1];
-            }
+            const int n = n0 + e < N ? n0 + e : N - 1;
+            if (!FP8 && !RAW && wave >= 4)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rsw, (lds_ptr_t)(lds + PSCALES + 1024 + 256 * (wave - 4)), 4,
+                                                         (uint32_t)n * 4u, 0, 0, 0);
+            if (BIAS && wave < 4)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(rbi, (lds_ptr_t)(lds + PSCALES + 2048 + 256 * wave), 4,
+                                                         (uint32_t)n * 4u, 0, 0, 0);
         }
 #pragma unroll
-        for (int j = 0; j < FN; j++) acc[j] = i32x16{};
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < TFN; j++) acc[i][j] = acc_t{0, 0, 0, 0};
         for (int kt = 0; kt < nk; kt++) {
             const int cur = buf;
-            __builtin_amdgcn_sched_barrier(0);
             if (kt + 1 < nk) {
                 dload(cur ^ 1, ga, gw, (kt + 1) * TBK);
             } else {       // the next tile's stage 0 (this tile's again if there is none)
                 if (has_next) addr(tnext, ga, gw);
                 dload(cur ^ 1, ga, gw, 0);
             }
-            rd(1, cur, 1);
-            mm(0);
-            pattern(true);
-            __builtin_amdgcn_sched_barrier(0);
-            rd(0, cur, 2);
-            mm(1);
-            pattern(false);
-            __builtin_amdgcn_sched_barrier(0);
-            rd(1, cur, 3);
-            mm(0);
-            pattern(false);
-            __builtin_amdgcn_sched_barrier(0);
-            // next stage landed and this wave's reads of this stage are done
-            __builtin_amdgcn_s_waitcnt(0x0070);
-            __builtin_amdgcn_s_barrier();
-            __builtin_amdgcn_sched_barrier(0);
-            rd(0, cur ^ 1, 0);
-            mm(1);
-            pattern(false);
-            __builtin_amdgcn_sched_barrier(0);
+            if (!FP8) {
+                rdh(h1a, h1w, cur, 1);
+                mmh(h0a, h0w);
+                // the next stage landed and every wave's reads of this one are done
+                __builtin_amdgcn_s_waitcnt(0x0070);
+                __builtin_amdgcn_s_barrier();
+                rdh(h0a, h0w, cur ^ 1, 0);
+                mmh(h1a, h1w);
+            } else {
+                const int8_t* ab = arow + cur * TLDS_STAGE;
+                const int8_t* wb = wrow + cur * TLDS_STAGE;
+                // lane group q takes 16-byte chunks q and q + 4 of the row (the
+                // k order of the 8-bit operands of the f8f6f4 instruction)
+                i32x8 fa[FM], fw[TFN];
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+                    const i32x4 lo = lds16(ab + i * 16 * TBK + (((2 * q) ^ sw) << 4));
+                    const i32x4 hi = lds16(ab + i * 16 * TBK + (((2 * q + 1) ^ sw) << 4));
+                    fa[i] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int j = 0; j < TFN; j++) {
+                    const i32x4 lo = lds16(wb + j * 16 * TBK + (((2 * q) ^ sw) << 4));
+                    const i32x4 hi = lds16(wb + j * 16 * TBK + (((2 * q + 1) ^ sw) << 4));
+                    fw[j] = i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                }
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < TFN; j++)
+                        acc[i][j] = (acc_t)__builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                            fa[i], fw[j], (f32x4)acc[i][j], 0, 0, 0, 0, 0, 0);
+                // the next stage landed and every wave's reads of this one are done
+                __builtin_amdgcn_s_waitcnt(0x0070);
+                __builtin_amdgcn_s_barrier();
+            }
             buf = cur ^ 1;
         }
-        // buffer buf ^ 1 (this tile's last stage) is free; buffer buf holds the
-        // next tile's stage 0 and fa/fw[0] its first fragments
+        // buffer buf holds the next tile's stage 0; buffer buf ^ 1 is free
         if (RAW) {   // int32 accumulators (bit-exactness checks): direct stores
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int n = n0 + j * 32 + r32;
-                if (n >= N) continue;
+            for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int v = 0; v < 16; v++) {    // 32x32 C layout: row 8 (v/4) + 4 (l/32) + v%4
-                    const int m = m0 + wave * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
-                    if (m < M) Craw[(size_t)m * N + n] = acc[j][v];
+                for (int j = 0; j < TFN; j++) {
+                    const int n = n0 + wn * 112 + j * 16 + r16;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
+                        if (m < M && n < N) Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
+                    }
                 }
+            if (!has_next) break;
+            t = tnext;
+            continue;
+        }
+        uint16_t* ct = reinterpret_cast<uint16_t*>(lds + (buf ^ 1) * TLDS_STAGE) + wave * (32 * PCROW);
+        const float* lsc = reinterpret_cast<const float*>(lds + PSCALES);
+        float swv[TFN], bv[TFN];
+#pragma unroll
+        for (int j = 0; j < TFN; j++) {
+            const int c = wn * 112 + j * 16 + r16;
+            swv[j] = FP8 ? sw8 : lsc[256 + c];
+            bv[j] = BIAS ? lsc[512 + c] : 0.0f;
+        }
+#pragma unroll
+        for (int p = 0; p < 2; p++) {         // fragment rows 2p, 2p + 1: wave rows 32 p .. 32 p + 31
+#pragma unroll
+            for (int i = 2 * p; i < 2 * p + 2; i++) {
+                const f32x4 sa = FP8 ? f32x4{sa8, sa8, sa8, sa8}
+                                     : *reinterpret_cast<const f32x4*>(lsc + wm * 64 + i * 16 + q * 4);
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        ct[((i - 2 * p) * 16 + q * 4 + e) * PCROW + j * 16 + r16] =
+                            BIAS ? bf16_out((float)acc[i][j][e] * sa[e] * swv[j] + bv[j])
+                                 : bf16_out((float)acc[i][j][e] * sa[e] * swv[j]);
             }
-        } else {
-            uint16_t* ct = reinterpret_cast<uint16_t*>(lds + (buf ^ 1) * TLDS_STAGE) + wave * (16 * XCROW);
-            // the bias is read here rather than before the K loop (the loop
-            // already holds every register), and only in the BIAS build
-            float bv[FN];
 #pragma unroll
-            for (int j = 0; j < FN; j++) {
-                const int n = n0 + j * 32 + r32;
-                bv[j] = BIAS ? bias[n < N ? n : N - 1] : 0.0f;
-            }
-#pragma unroll
-            for (int p = 0; p < 2; p++) {         // rows 16 p .. 16 p + 15 of the wave's 32
-#pragma unroll
-                for (int j = 0; j < FN; j++)
-#pragma unroll
-                    for (int v = 8 * p; v < 8 * p + 8; v++)
-                        ct[(8 * (v >> 2) + 4 * h + (v & 3) - 16 * p) * XCROW + j * 32 + r32] =
-                            BIAS ? bf16_out((float)acc[j][v] * sa[v] * swv[j] + bv[j])
-                                 : bf16_out((float)acc[j][v] * sa[v] * swv[j]);
-#pragma unroll
-                for (int q = 0; q < 7; q++) {     // 16 rows x 28 pieces of 16 B = 7 x 64
-                    const int qd = q * 64 + lane;
-                    const int row = qd / 28, c = qd - row * 28;
-                    const int m = m0 + wave * 32 + 16 * p + row, n = n0 + c * 8;
-                    const i32x4 val = *reinterpret_cast<const i32x4*>(ct + row * XCROW + c * 8);
-                    const uint32_t off = (m < M && n < N) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 2u : BUF_DROP;
-                    __builtin_amdgcn_raw_buffer_store_b128(val, ro, off, 0, 0);
-                }
+            for (int c = 0; c < 7; c++) {     // 32 rows x 14 pieces of 16 B = 7 x 64
+                const int qd = c * 64 + lane;
+                const int row = qd / 14, pc = qd - row * 14;
+                const int m = m0 + wm * 64 + 32 * p + row, n = n0 + wn * 112 + pc * 8;
+                const i32x4 val = *reinterpret_cast<const i32x4*>(ct + row * PCROW + pc * 8);
+                const uint32_t off = (m < M && n < N) ? ((uint32_t)m * (uint32_t)N + (uint32_t)n) * 2u : BUF_DROP;
+                __builtin_amdgcn_raw_buffer_store_b128(val, ro, off, 0, 0);
             }
         }
-        // staging reads done (lgkmcnt(0)) before the next tile reloads this buffer
+        // staging reads done (lgkmcnt(0)) before the next tile loads into this buffer
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_s_barrier();
         if (!has_next) break;
@@ -1013,8 +1054,8 @@ __global__ void __launch_bounds__(512) k_gemm_i8p(const int8_t* __restrict__ A,
     __builtin_amdgcn_s_waitcnt(0x0070);       // the spare stage-0 loads land before exit
 }
 
-template <bool RAW, bool BIAS>
-int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
+template <bool FP8, bool RAW, bool BIAS>
+int launch_8wp(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
                uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const int ntiles = tiles_m * tiles_n;
@@ -1022,16 +1063,16 @@ int launch_i8p(const int8_t* A, const int8_t* W, const float* sA, const float* s
     // one workgroup per CU (rounded down to a multiple of 8: tiles keep their XCD)
     int grid = ncu >= 8 ? ncu - ncu % 8 : ncu;
     if (grid > ntiles) grid = ntiles;
-    const size_t lds = 2 * (size_t)TLDS_STAGE;
+    const size_t lds = PLDS;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_gemm_i8p<RAW, BIAS>);
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8wp<FP8, RAW, BIAS>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_gemm_i8p<RAW, BIAS><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m,
-                                                  tiles_n);
-    return snx_launch_check("k_gemm_i8p");
+    k_gemm_8wp<FP8, RAW, BIAS><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m,
+                                                       tiles_n);
+    return snx_launch_check("k_gemm_8wp");
 }
 
 template <bool FP8, bool RAW, bool BIAS>
@@ -1090,11 +1131,11 @@ int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float
         // and writes bf16 output in 16-byte row pieces
         const bool fits = (uint64_t)M * K < (1ull << 31) && (uint64_t)N * K < (1ull << 31);
         if (c_i32)
-            return fits ? launch_i8p<true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+            return fits ? launch_8wp<false, true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
                         : launch_x32<false, true, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
         if (fits && N % 8 == 0 && (reinterpret_cast<uintptr_t>(out_bf16) & 15) == 0 && (uint64_t)M * N * 2 < BUF_DROP)
-            return bias ? launch_i8p<false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
-                        : launch_i8p<false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
+            return bias ? launch_8wp<false, false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+                        : launch_8wp<false, false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
         return bias ? launch_x32<false, false, true>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
                     : launch_x32<false, false, false>(A, W, sA, sW, c_i32, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
     }
@@ -1145,6 +1186,10 @@ int snx_k_fp8_gemm(const uint8_t* A, const uint8_t* W, const float* sA, const fl
     if (K % TBK == 0 && M >= 128 && N >= 128) {
         const int8_t* a8 = reinterpret_cast<const int8_t*>(A);
         const int8_t* w8 = reinterpret_cast<const int8_t*>(W);
+        if (N % 8 == 0 && (reinterpret_cast<uintptr_t>(out_bf16) & 15) == 0 && (uint64_t)M * N * 2 < BUF_DROP &&
+            (uint64_t)M * K < (1ull << 31) && (uint64_t)N * K < (1ull << 31))
+            return bias ? launch_8wp<true, false, true>(a8, w8, sA, sW, nullptr, out_bf16, bias, (int)M, (int)N, (int)K, S(st))
+                        : launch_8wp<true, false, false>(a8, w8, sA, sW, nullptr, out_bf16, bias, (int)M, (int)N, (int)K, S(st));
         if (bias)
             return launch_tiled<true, false, true>(a8, w8, sA, sW, nullptr, out_bf16, bias, (int)M, (int)N,
                                                    (int)K, S(st));
