@@ -52,7 +52,7 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "decode", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "decode", "shard", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -194,28 +194,39 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
 LLAMA3_LINEARS = {"qkv": (6144, 4096), "o": (4096, 4096), "gate_up": (28672, 4096), "down": (4096, 14336)}
 
 
-def bench_decode(lib, timer, torch, copies, steps, warmup, layer):
+def llama_linears(tp=1):
+    """[N, K] of the Llama-3-8B layer's linears on one GPU of a tp-way
+    tensor-parallel layer: QKV and gate/up column-parallel (N / tp), O and
+    down row-parallel (K / tp)."""
+    return {"qkv": (6144 // tp, 4096), "o": (4096, 4096 // tp), "gate_up": (28672 // tp, 4096),
+            "down": (4096, 14336 // tp)}
+
+
+def bench_decode(lib, timer, torch, copies, steps, warmup, layer, tp=1):
     """One token (M = 1) through C5's Llama-3-8B linears: the gate/up
     projection with its SwiGLU step as one launch (layer False), or the
     layer's four linears back to back (QKV, O, gate/up + SwiGLU, down; the
     attention and norms between them are not part of it), weights rotated
-    over `copies` copies so they stream from HBM."""
-    H, F = 4096, 14336
-    names = list(LLAMA3_LINEARS) if layer else ["gate_up"]
+    over `copies` copies so they stream from HBM.  tp > 1: one GPU's shard
+    of a tp-way tensor-parallel layer (the reductions after O and down are
+    not part of it)."""
+    shapes = llama_linears(tp)
+    H, QKV, A, F = 4096, shapes["qkv"][0], shapes["o"][1], shapes["gate_up"][0] // 2
+    names = list(shapes) if layer else ["gate_up"]
     ws = {}
-    for i, (n, (N, K)) in enumerate(LLAMA3_LINEARS.items()):
+    for i, (n, (N, K)) in enumerate(shapes.items()):
         if n in names:
             ws[n], _ = make_w4(lib, N, K, 128, copies, 40 + i, torch)
     g = torch.Generator(device="cuda").manual_seed(47)
     x = torch.randn((1, H), device="cuda", generator=g).to(torch.bfloat16)
     bufs = {n: torch.empty((1, N), dtype=torch.bfloat16, device="cuda")
-            for n, N in (("qkv", 6144), ("o", H), ("h", F), ("y", H))}
+            for n, N in (("qkv", QKV), ("o", H), ("h", F), ("y", H))}
     st = timer.stream
     # copy c, linear j at [4 c + j]; absent linears repeat gate/up (never read)
-    flat = [ws[n][c] if n in ws else ws["gate_up"][c] for c in range(copies) for n in LLAMA3_LINEARS]
+    flat = [ws[n][c] if n in ws else ws["gate_up"][c] for c in range(copies) for n in shapes]
     qwa, sca, qza = (ptr_array([t[i] for t in flat]) for i in range(3))
     loop = make_loop("snxb_loop_decode", C.c_int(copies), C.c_int(1 if layer else 0), x, qwa, sca, qza,
-                     bufs["qkv"], bufs["o"], bufs["h"], bufs["y"], H, 6144, F, C.c_void_p(st))
+                     bufs["qkv"], bufs["o"], bufs["h"], bufs["y"], H, QKV, F, A, C.c_void_p(st))
 
     def step(c):
         calls = []
@@ -223,9 +234,9 @@ def bench_decode(lib, timer, torch, copies, steps, warmup, layer):
         if layer:
             q, o, d = ws["qkv"][c], ws["o"][c], ws["down"][c]
             calls.append(bound(lib, "SNEPPX_qlinear_w4a16", x, q[0], q[1], q[2], None, 0, None, bufs["qkv"],
-                               SNEPPX_BFLOAT16, 1, 6144, H, 128, C.c_void_p(st)))
+                               SNEPPX_BFLOAT16, 1, QKV, H, 128, C.c_void_p(st)))
             calls.append(bound(lib, "SNEPPX_qlinear_w4a16", bufs["qkv"], o[0], o[1], o[2], None, 0, None,
-                               bufs["o"], SNEPPX_BFLOAT16, 1, H, H, 128, C.c_void_p(st)))
+                               bufs["o"], SNEPPX_BFLOAT16, 1, H, A, 128, C.c_void_p(st)))
         calls.append(bound(lib, "SNEPPX_qlinear_w4a16_swiglu", bufs["o"] if layer else x, gu[0], gu[1], gu[2],
                            None, bufs["h"], 1, F, H, 128, C.c_void_p(st)))
         if layer:
@@ -233,11 +244,11 @@ def bench_decode(lib, timer, torch, copies, steps, warmup, layer):
                                bufs["y"], SNEPPX_BFLOAT16, 1, H, F, 128, C.c_void_p(st)))
         return lambda: [f() for f in calls]
     total, mean_step, _ = timer.run([step(c) for c in range(copies)], steps, warmup, loop)
-    nbytes = sum(w4_bytes(1, N, K, K // 128) for n, (N, K) in LLAMA3_LINEARS.items() if n in names)
+    nbytes = sum(w4_bytes(1, N, K, K // 128) for n, (N, K) in shapes.items() if n in names)
     nbytes -= 2 * F if "gate_up" in names else 0        # gate/up writes F outputs, not 2 F
     host = {n: tuple(t.cpu() for t in ws[n][0]) for n in names}
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
-            "host": {"w": host, "x": _u16(x)}}
+            "host": {"w": host, "x": _u16(x), "shapes": shapes}}
 
 
 def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
@@ -422,16 +433,19 @@ def llama_tokens(seed=5):
     return 16 + int(lens.sum()), [int(v) for v in lens]
 
 
-def bench_chain(lib, timer, torch, steps, warmup):
+def bench_chain(lib, timer, torch, steps, warmup, tp=1):
     """C5: one Llama-3-8B decoder layer's linears in W4A16 g128 (AWQ-style,
     random init): QKV 4096->6144, O 4096->4096, gate/up 4096->2x14336 with
     SiLU(gate)*up in the GEMM's epilogue, down 14336->4096, on T packed
     tokens.  The O input is a
     synthetic bf16 tensor (attention is not part of this path); the gate/up
-    input is the O output."""
+    input is the O output.  tp > 1: one GPU's shard of a tp-way
+    tensor-parallel layer (QKV, gate/up N / tp; O, down K / tp; the
+    reductions after O and down are not part of it)."""
     T, lens = llama_tokens()
-    H, F = 4096, 14336
-    shapes = {"qkv": (6144, H), "o": (H, H), "gate_up": (2 * F, H), "down": (H, F)}
+    H = 4096
+    shapes = llama_linears(tp)
+    F, A = shapes["gate_up"][0] // 2, shapes["o"][1]
     g = torch.Generator(device="cuda").manual_seed(17)
     ws = {}
     for name, (N, K) in shapes.items():
@@ -444,8 +458,8 @@ def bench_chain(lib, timer, torch, steps, warmup):
         del w
         ws[name] = (qw, sc, qz, G)
     x = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
-    attn = torch.randn((T, H), device="cuda", generator=g).to(torch.bfloat16)
-    y_qkv = torch.empty((T, 6144), dtype=torch.bfloat16, device="cuda")
+    attn = torch.randn((T, A), device="cuda", generator=g).to(torch.bfloat16)
+    y_qkv = torch.empty((T, shapes["qkv"][0]), dtype=torch.bfloat16, device="cuda")
     y_o = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
     y_gu = torch.empty((T, 2 * F), dtype=torch.bfloat16, device="cuda")
     act = torch.empty((T, F), dtype=torch.bfloat16, device="cuda")
@@ -486,6 +500,82 @@ def bench_chain(lib, timer, torch, steps, warmup):
 
 
 CPU_ROWS = 16     # activation rows of the C4 / C5 CPU slices
+
+SHARD_TP = 8      # the tensor-parallel degree whose per-GPU shapes the shard lines measure
+
+
+def _copies_for(nbytes, floor=16):
+    """Rotating weight copies that together exceed the 256 MB Infinity Cache
+    with room to spare (>= 320 MB), so every call streams from HBM."""
+    return max(floor, -(-320_000_000 // nbytes))
+
+
+def bench_shards(lib, timer, torch, steps, warmup, tp=SHARD_TP, log=None):
+    """Every config at one GPU's share of a tp-way tensor-parallel layer: the
+    decode GEMVs and the W8A8 GEMM column-parallel (N / tp), the Llama-3-8B
+    layer's QKV and gate/up column-parallel and O and down row-parallel
+    (K / tp).  The collectives that would join the shards are not part of
+    it.  Returns (extra entries, CPU jobs)."""
+    out, jobs = [], []
+    tag = f"TP={tp} shard: "
+    N2, K = 11008 // tp, 4096
+    for m in (1, 16):
+        cp = _copies_for(w4_bytes(m, N2, K, K // 128))
+        r, (ws_m, x_m, _, _) = bench_w4a16(lib, timer, torch, m, N2, K, 128, cp, steps, warmup)
+        out.append({"workload": f"{tag}C2 W4A16 g128 GEMV N={N2} K={K} M={m}", "value": round(r["gbs"], 1),
+                    "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                    "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
+                    "weight_copies": cp})
+        jobs.append((out[-1], "w4", {"qw": _u32(ws_m[0][0]), "sc": _u16(ws_m[0][1]), "qz": _u32(ws_m[0][2]),
+                                     "x": _u16(x_m), "bytes": r["bytes"]}))
+        del ws_m, x_m
+    cp = _copies_for(w4_bytes(1, N2, K, K // 128, zeros=False))
+    r = bench_w4a16_gptq(lib, timer, torch, 1, N2, K, cp, steps, warmup)
+    out.append({"workload": f"{tag}C3 GPTQ act-order W4A16 (prepared) N={N2} K={K} M=1",
+                "value": round(r["gbs"], 1), "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
+                "weight_copies": cp})
+    jobs.append((out[-1], "w4_gidx", dict(r["host"], bytes=r["bytes"])))
+    N1 = 4096 // tp
+    cp = _copies_for(N1 * K)
+    r = bench_w8(lib, timer, torch, N1, K, cp, steps, warmup)
+    out.append({"workload": f"{tag}C1 W8 weight-only GEMV N={N1} K={K} M=1 fp32", "value": round(r["gbs"], 1),
+                "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+                "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
+                "weight_copies": cp})
+    jobs.append((out[-1], "w8", r["host"]))
+    sh = llama_linears(tp)
+    for layer in (False, True):
+        per_copy = sum(w4_bytes(1, N, K_, K_ // 128) for n, (N, K_) in sh.items() if layer or n == "gate_up")
+        cp = _copies_for(per_copy)
+        r = bench_decode(lib, timer, torch, cp, steps, warmup, layer, tp=tp)
+        what = ("Llama-3-8B layer linears at decode (QKV {qkv[0]}x{qkv[1]}, O {o[0]}x{o[1]}, gate/up "
+                "{gate_up[0]}x{gate_up[1]} + SwiGLU fused, down {down[0]}x{down[1]}; 4 launches)".format(**sh)
+                if layer else f"Llama-3-8B gate/up projection + SwiGLU fused, one launch "
+                              f"(F={sh['gate_up'][0] // 2}, K={sh['gate_up'][1]})")
+        out.append({"workload": f"{tag}{what} W4A16 g128 M=1", "value": round(r["gbs"], 1), "unit": "GB/s",
+                    "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "bytes": r["bytes"],
+                    "ms_per_step": round(r["ms_per_step"], 5), "weight_copies": cp})
+        jobs.append((out[-1], "decode", dict(r["host"], bytes=r["bytes"], layer=layer)))
+    r = bench_chain(lib, timer, torch, 10, 30, tp=tp)
+    out.append({"workload": f"{tag}C5 Llama-3-8B layer W4A16 g128 linear chain T={r['T']}",
+                "value": round(r["tflops"], 1), "unit": "TFLOP/s",
+                "frac_of_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
+                "ms_per_step": round(r["ms_per_step"], 4), "steps": 10, "warmup": 30,
+                "per_linear": r["per_linear"]})
+    jobs.append((out[-1], "chain", dict(r["host"], T=r["T"], flops=r["flops"])))
+    N4 = 14336 // tp
+    for fp8 in (False, True):
+        r = bench_w8a8(lib, timer, torch, 2048, N4, 4096, GEMM_STEPS, GEMM_WARMUP, fp8=fp8)
+        peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS
+        out.append({"workload": f"{tag}C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N={N4} K=4096",
+                    "value": round(r["tops"], 1), "unit": "TOPS", "frac_of_peak": round(r["tops"] / peak, 4),
+                    "ms_per_step": round(r["ms_per_step"], 4), "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
+        jobs.append((out[-1], "fp8" if fp8 else "i8", r["host"]))
+    if log:
+        for e in out:
+            log(f"[bench] {e['workload']}: {e['value']} {e['unit']} ({e['frac_of_peak']})")
+    return out, jobs
 
 
 def _u32(t):
@@ -557,26 +647,28 @@ def cpu_legs(orc, jobs, seconds):
                                                f"{A.shape[0]} of {M} rows of A against all of W, "
                                                f"{per:.2f} s per slice, extrapolated linearly to M={M} "
                                                f"({full:.0f} s per call)")
-        elif kind == "decode":                 # C5 linears at M = 1, full shapes
+        elif kind == "decode":                 # C5 linears at M = 1 (full or one shard's shapes)
             w = {n: (v[0].numpy().view(np.uint32), v[1].numpy().view(np.uint16), v[2].numpy().view(np.uint32))
                  for n, v in h["w"].items()}
+            sh = h["shapes"]
 
             def token():
                 xs = h["x"]
                 if h["layer"]:
-                    rc, q = orc.w4a16_linear(xs, *w["qkv"], None, 6144, 4096, 128)
-                    xs = _bf16_np(q[:, :4096])
-                    rc, o = orc.w4a16_linear(xs, *w["o"], None, 4096, 4096, 128)
+                    rc, q = orc.w4a16_linear(xs, *w["qkv"], None, *sh["qkv"], 128)
+                    xs = _bf16_np(q[:, :sh["o"][1]])
+                    rc, o = orc.w4a16_linear(xs, *w["o"], None, *sh["o"], 128)
                     xs = _bf16_np(o)
-                rc, gu = orc.w4a16_linear(xs, *w["gate_up"], None, 28672, 4096, 128)
-                g = gu[:, :14336]
+                rc, gu = orc.w4a16_linear(xs, *w["gate_up"], None, *sh["gate_up"], 128)
+                F = sh["gate_up"][0] // 2
+                g = gu[:, :F]
                 with np.errstate(over="ignore"):
-                    act = _bf16_np((g / (np.float32(1) + np.exp(-g)) * gu[:, 14336:]).astype(np.float32))
+                    act = _bf16_np((g / (np.float32(1) + np.exp(-g)) * gu[:, F:]).astype(np.float32))
                 if h["layer"]:
-                    orc.w4a16_linear(act, *w["down"], None, 4096, 14336, 128)
+                    orc.w4a16_linear(act, *w["down"], None, *sh["down"], 128)
             per, reps, el = _per_call(token, seconds, max_reps=20)
             entry["cpu_baseline"] = _cpu_entry(round(h["bytes"] / per / 1e9, 4), "GB/s",
-                                               f"full shapes M=1, {reps} calls in {el:.1f} s "
+                                               f"the same shapes M=1, {reps} calls in {el:.1f} s "
                                                f"({per * 1e3:.1f} ms/call)")
         elif kind == "mx":                     # MX GEMM: decode W once, rows of A extrapolated
             sys.path.insert(0, os.path.join(REPO, "oracle"))
@@ -608,7 +700,7 @@ def cpu_legs(orc, jobs, seconds):
                     N, K = shapes[name]
                     orc.w4a16_linear(inp, *w[name], None, N, K, 128)
                 N, K = shapes["gate_up"]
-                rc, gu = orc.w4a16_linear(at, *w["gate_up"], None, N, K, 128)
+                rc, gu = orc.w4a16_linear(xs, *w["gate_up"], None, N, K, 128)
                 F = N // 2
                 g = gu[:, :F]
                 with np.errstate(over="ignore"):
@@ -730,6 +822,9 @@ def run_only(args, lib, timer, torch, N, K, group):
         for fmt in MX_BENCH:
             r = bench_mx(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fmt)
             print(f"{fmt} gemm: {r['ms_per_step'] * 1e3:.1f} us, {r['tflops']:.0f} TFLOP/s")
+    elif args.only == "shard":
+        bench_shards(lib, timer, torch, max(50, steps // 4), 10,
+                     log=lambda t: print(t, flush=True))
     elif args.only == "chain":
         r = bench_chain(lib, timer, torch, steps, 2)
         print(f"chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s {r['per_linear']}")
@@ -866,6 +961,11 @@ def main():
                 print(f"[bench] {extra[-1]['workload']}: {r['tflops']:.0f} TFLOP/s", file=sys.stderr, flush=True)
                 if not kept:
                     cpu_jobs.append((extra[-1], "mx", r["host"]))
+        # one GPU's share of a tensor-parallel layer (the collectives are not part of it)
+        shard, shard_jobs = bench_shards(lib, timer, torch, max(50, args.steps // 4), 10,
+                                         log=lambda t: print(t, file=sys.stderr, flush=True))
+        extra.extend(shard)
+        cpu_jobs.extend(shard_jobs)
 
     cpu = None
     if not args.no_cpu:

@@ -829,7 +829,21 @@ constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every outpu
 //    only what it wrote, so no barrier sits between staging and stores.
 // Requires N % 8 == 0 (a 16-byte piece never straddles a row end), a 16-byte
 // aligned output below 2 GiB and operands below 2 GiB.
-constexpr int PCROW = 120;   // u16 per staged output row of a wave: 112 + 8 pad
+// SPLIT > 1 (shapes with too few tiles to fill the CUs, such as one GPU's
+// column shard of a tensor-parallel layer): a work unit is (tile, K span s)
+// with spans of K / SPLIT; unit v covers tile v % ntiles, span v / ntiles.
+// After its K loop each wave stores its accumulators to its slot of `part`
+// (lane-major, 1 KB per store instruction) with the system-coherent cache
+// policy (written through the XCD's L2), waits until they are written, and
+// counts itself in cnt[tile][wave].  The wave that arrives last adds the
+// SPLIT slots of its (tile, wave) in span order (0, 1, ...: the same fp32
+// sums whichever wave is last), returns the counter to 0 for the next call
+// and runs the epilogue; the others skip it.  The last wave reads the slots
+// with the same policy, so no copy an L2 holds is used, and no fence has to
+// write back or drop whole caches.  No wave waits for another, so
+// the result does not depend on which units are resident together.
+constexpr int PCROW = 120;
+constexpr int kSysCoherent = 1 | 16;   // buffer cache policy sc0 sc1: system-coherent access   // u16 per staged output row of a wave: 112 + 8 pad
 static_assert(8 * 32 * PCROW * 2 <= TLDS_STAGE, "a pass of every wave fits in one stage buffer");
 // A tile's int8 row / column scales and its bias wait in LDS beside the ring
 // (256 floats each, loaded straight from global memory when the tile starts)
@@ -837,7 +851,7 @@ static_assert(8 * 32 * PCROW * 2 <= TLDS_STAGE, "a pass of every wave fits in on
 constexpr int PSCALES = 2 * TLDS_STAGE;
 constexpr int PLDS = PSCALES + 3 * 256 * 4;
 
-template <bool FP8, bool RAW, bool BIAS>
+template <bool FP8, bool RAW, bool BIAS, int SPLIT = 1>
 __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
                                                   const int8_t* __restrict__ W,
                                                   const float* __restrict__ sA,
@@ -845,7 +859,8 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
                                                   int32_t* __restrict__ Craw,
                                                   uint16_t* __restrict__ out,
                                                   const float* __restrict__ bias, int M, int N,
-                                                  int K, int tiles_m, int tiles_n) {
+                                                  int K, int tiles_m, int tiles_n,
+                                                  i32x4* __restrict__ part, uint32_t* __restrict__ cnt) {
     constexpr int FM = 4;
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -853,20 +868,23 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
     const int wm = wave >> 1, wn = wave & 1;
     const int r16 = lane & 15, q = lane >> 4;
     const int b = blockIdx.x, nb = gridDim.x;
-    const int ntiles = tiles_m * tiles_n;
+    const int ntiles = tiles_m * tiles_n, nunits = ntiles * SPLIT;
     const int lrow = lane >> 3, lslot = lane & 7;
-    auto tile_of = [&](int t) { return (ntiles % 8 == 0) ? (t % 8) * (ntiles / 8) + t / 8 : t; };
+    // unit of walk position t (each XCD a compact block of units), its tile and K span
+    auto unit_of = [&](int t) { return (nunits % 8 == 0) ? (t % 8) * (nunits / 8) + t / 8 : t; };
+    auto tile_of = [&](int t) { return SPLIT == 1 ? unit_of(t) : unit_of(t) % ntiles; };
     auto addr = [&](int t, uint32_t* ga, uint32_t* gw) {
         const int tl = tile_of(t);
         const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
+        const uint32_t kb = SPLIT == 1 ? 0u : (uint32_t)(unit_of(t) / ntiles) * (uint32_t)(K / SPLIT);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int row = (8 * i + wave) * 8 + lrow;
             const int gr = m0 + row < M ? m0 + row : M - 1;
-            ga[i] = (uint32_t)gr * (uint32_t)K + (uint32_t)((lslot ^ swz(row)) * 16);
+            ga[i] = (uint32_t)gr * (uint32_t)K + kb + (uint32_t)((lslot ^ swz(row)) * 16);
             const int wr = row < TBN ? row : TBN - 1;
             const int gn = n0 + wr < N ? n0 + wr : N - 1;
-            gw[i] = (uint32_t)gn * (uint32_t)K + (uint32_t)((lslot ^ swz(wr)) * 16);
+            gw[i] = (uint32_t)gn * (uint32_t)K + kb + (uint32_t)((lslot ^ swz(wr)) * 16);
         }
     };
     const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc((void*)A, (short)0, M * K, 0x00020000);
@@ -891,7 +909,7 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
     const int sw = swz(r16);
     const int8_t* arow = lds + (wm * 64 + r16) * TBK;
     const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
-    const int nk = K / TBK;
+    const int nk = K / SPLIT / TBK;
 
     // int8: each k-step is two halves h (the even / odd 16-byte chunks, the
     // same bank pattern as the fp8 reads; any k order works as long as A and
@@ -915,7 +933,7 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
     };
 
     int t = b;
-    if (t >= ntiles) return;
+    if (t >= nunits) return;
     const float sa8 = FP8 ? sA[0] : 0.0f, sw8 = FP8 ? sW[0] : 0.0f;   // fp8: per-tensor scales
     uint32_t ga[4], gw[4];
     addr(t, ga, gw);
@@ -928,7 +946,7 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
         const int tl = tile_of(t);
         const int m0 = (tl % tiles_m) * TBM, n0 = (tl / tiles_m) * TBN;
         const int tnext = t + nb;
-        const bool has_next = tnext < ntiles;
+        const bool has_next = tnext < nunits;
         // this tile's scales / bias into LDS (landed by the first k-step's wait)
         {
             const int e = 64 * (wave & 3) + lane;
@@ -996,6 +1014,75 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
             buf = cur ^ 1;
         }
         // buffer buf holds the next tile's stage 0; buffer buf ^ 1 is free
+        bool last = true;
+        if (SPLIT > 1) {
+            // slot (unit, wave): FM x TFN x 64 lanes x 16 B, lane-major; buffer
+            // accesses with the wave-uniform part of the address in soffset
+            constexpr int SLOTB = FM * TFN * 64 * 16;
+            const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)part, (short)0, nunits * 8 * SLOTB, 0x00020000);
+            const int sp = unit_of(t) / ntiles;
+            const uint32_t mine = (uint32_t)((sp * ntiles + tl) * 8 + wave) * SLOTB;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < TFN; j++)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(i32x4, acc[i][j]), rp, lane * 16,
+                                                           mine + (i * TFN + j) * 1024, kSysCoherent);
+            // the slot is written before it is counted; and nothing may write
+            // the accumulator registers before the stores have read them (a
+            // 16-byte store reads its data after issue): the scheduler may not
+            // move the next instructions above this wait
+            __builtin_amdgcn_sched_barrier(0);
+            __builtin_amdgcn_s_waitcnt(0x0f70);           // vmcnt(0)
+            __builtin_amdgcn_sched_barrier(0);
+            uint32_t c = 0;
+            if (lane == 0) c = atomicAdd(&cnt[tl * 8 + wave], 1u);
+            last = __builtin_amdgcn_readfirstlane(c) == SPLIT - 1;
+            if (last) {
+                const uint32_t first = (uint32_t)(tl * 8 + wave) * SLOTB, sstride = (uint32_t)ntiles * 8 * SLOTB;
+                // in chunks of 4 fragments x SPLIT spans: the loads of a chunk in
+                // flight together, and each chunk's offsets carry a zero that the
+                // previous chunk's sums produce (an opaque dependency), so that
+                // the compiler cannot hoist every load and spill the sums
+                constexpr int JC = 4;
+                uint32_t dep = 0;
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+#pragma unroll
+                    for (int j0 = 0; j0 < TFN; j0 += JC) {
+                        i32x4 v[SPLIT][JC];
+#pragma unroll
+                        for (int s2 = 0; s2 < SPLIT; s2++)
+#pragma unroll
+                            for (int jj = 0; jj < JC; jj++)
+                                if (j0 + jj < TFN)
+                                    v[s2][jj] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                        rp, lane * 16, first + dep + s2 * sstride + (i * TFN + j0 + jj) * 1024,
+                                        kSysCoherent));
+#pragma unroll
+                        for (int jj = 0; jj < JC; jj++) {
+                            if (j0 + jj >= TFN) break;
+                            acc_t r = __builtin_bit_cast(acc_t, v[0][jj]);
+#pragma unroll
+                            for (int s2 = 1; s2 < SPLIT; s2++) r += __builtin_bit_cast(acc_t, v[s2][jj]);
+                            acc[i][j0 + jj] = r;
+                        }
+                        if (j0 + JC <= TFN)
+                            asm volatile("s_mov_b32 %0, 0"
+                                         : "=s"(dep)
+                                         : "v"(acc[i][j0]), "v"(acc[i][j0 + 1]), "v"(acc[i][j0 + 2]),
+                                           "v"(acc[i][j0 + 3]));
+                        else
+                            asm volatile("s_mov_b32 %0, 0"
+                                         : "=s"(dep)
+                                         : "v"(acc[i][j0]), "v"(acc[i][j0 + 1 < TFN ? j0 + 1 : j0]),
+                                           "v"(acc[i][j0 + 2 < TFN ? j0 + 2 : j0]));
+                    }
+                }
+                if (lane == 0) atomicExch(&cnt[tl * 8 + wave], 0u);   // ready for the next call
+            }
+        }
         if (RAW) {   // int32 accumulators (bit-exactness checks): direct stores
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -1005,7 +1092,7 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
 #pragma unroll
                     for (int e = 0; e < 4; e++) {
                         const int m = m0 + wm * 64 + i * 16 + q * 4 + e;
-                        if (m < M && n < N) Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
+                        if (last && m < M && n < N) Craw[(size_t)m * N + n] = ((i32x4)acc[i][j])[e];
                     }
                 }
             if (!has_next) break;
@@ -1023,6 +1110,7 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
         }
 #pragma unroll
         for (int p = 0; p < 2; p++) {         // fragment rows 2p, 2p + 1: wave rows 32 p .. 32 p + 31
+            if (!last) break;
 #pragma unroll
             for (int i = 2 * p; i < 2 * p + 2; i++) {
                 const f32x4 sa = FP8 ? f32x4{sa8, sa8, sa8, sa8}
@@ -1054,25 +1142,58 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
     __builtin_amdgcn_s_waitcnt(0x0070);       // the spare stage-0 loads land before exit
 }
 
+// K spans of the persistent kernel for M x N x K: 2 when the tiles fill at
+// most a quarter of the one-workgroup-per-CU grid and K splits into whole
+// 128-byte stages, else 1.  Measured (fp8, K = 4096, 256 CUs): 10, 32 and 64
+// tiles run 17-22 % faster in two spans; 128 tiles run 10 % slower, the
+// partials' traffic costing more than the CUs the spans bring in; four spans
+// were slower than two at 64 tiles (the last wave of a (tile, wave) reads
+// three 28 KB partial slots in round trips of one 16-load chunk).
+int w8a8_splits(int M, int N, int K) {
+    const int ntiles = ((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN);
+    const int ncu = snx::cu_count();
+    const int grid = ncu >= 8 ? ncu - ncu % 8 : ncu;
+    if (ntiles * 4 <= grid && K % (2 * TBK) == 0) return 2;
+    return 1;
+}
+
+template <bool FP8, bool RAW, bool BIAS, int SPLIT>
+int launch_8wp_s(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
+                 uint16_t* out, const float* bias, int M, int N, int K, int tiles_m, int tiles_n, int grid,
+                 i32x4* part, uint32_t* cnt, hipStream_t st) {
+    const size_t lds = PLDS;
+    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
+    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8wp<FP8, RAW, BIAS, SPLIT>);
+    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
+        snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
+        return -1;
+    }
+    k_gemm_8wp<FP8, RAW, BIAS, SPLIT><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m,
+                                                              tiles_n, part, cnt);
+    return snx_launch_check("k_gemm_8wp");
+}
+
 template <bool FP8, bool RAW, bool BIAS>
 int launch_8wp(const int8_t* A, const int8_t* W, const float* sA, const float* sW, int32_t* Craw,
                uint16_t* out, const float* bias, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const int ntiles = tiles_m * tiles_n;
     const int ncu = snx::cu_count();
-    // one workgroup per CU (rounded down to a multiple of 8: tiles keep their XCD)
+    const int split = w8a8_splits(M, N, K);
+    // one workgroup per CU (rounded down to a multiple of 8: units keep their XCD)
     int grid = ncu >= 8 ? ncu - ncu % 8 : ncu;
-    if (grid > ntiles) grid = ntiles;
-    const size_t lds = PLDS;
-    static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_gemm_8wp<FP8, RAW, BIAS>);
-    if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
-        snx_set_error("gemm: cannot reserve %zu bytes of LDS", lds);
-        return -1;
-    }
-    k_gemm_8wp<FP8, RAW, BIAS><<<grid, 512, lds, st>>>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m,
-                                                       tiles_n);
-    return snx_launch_check("k_gemm_8wp");
+    if (grid > ntiles * split) grid = ntiles * split;
+    if (split == 1)
+        return launch_8wp_s<FP8, RAW, BIAS, 1>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m, tiles_n, grid,
+                                              nullptr, nullptr, st);
+    // the span partials (one 229,376-byte slot per unit and wave group) and
+    // the arrival counters of the (tile, wave) pairs, which the kernel leaves at 0
+    const size_t slots = (size_t)ntiles * split * 8 * (4 * TFN * 64);
+    i32x4* part = static_cast<i32x4*>(snx_workspace(slots * sizeof(i32x4), 3, st));
+    uint32_t* cnt = static_cast<uint32_t*>(snx_workspace_zeroed((size_t)ntiles * 8 * sizeof(uint32_t), 4, st));
+    if (!part || !cnt) return -1;
+    return launch_8wp_s<FP8, RAW, BIAS, 2>(A, W, sA, sW, Craw, out, bias, M, N, K, tiles_m, tiles_n, grid, part,
+                                          cnt, st);
 }
 
 template <bool FP8, bool RAW, bool BIAS>

@@ -551,7 +551,13 @@ __global__ void __launch_bounds__(256) k_w4a16_gemv_small(const uint16_t* __rest
 // rows first) and y is bf16 [N] = silu(gate) * up: wave w of a workgroup
 // owning output rows [wg0, rend) (at most 8) computes gate row n = wg0 + w and
 // up row N + n as its two rows, and lane 63 applies the SwiGLU rule.
-template <int T, bool ZEROS, bool YF32, bool PERM, bool GLU = false>
+// KR (ragged K): K = Kr, a multiple of 256 in (2048 (T - 1), 2048 T); the
+// layout is the one of K = 2048 T, with the columns past K as padding: their
+// weight loads read zeros without a memory access, and their activations,
+// chunk sums and group scales are staged as zeros, so they add exactly 0.
+// Scales and zero words are then staged one 4-byte word per thread (rows of
+// K / 128 scales need not be 16-byte aligned).
+template <int T, bool ZEROS, bool YF32, bool PERM, bool GLU = false, bool KR = false>
 __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict__ x,
                                                      const uint32_t* __restrict__ qw,
                                                      const uint16_t* __restrict__ scales,
@@ -559,17 +565,20 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
                                                      const uint16_t* __restrict__ perm,
                                                      void* __restrict__ y,
                                                      const float* __restrict__ bias, int N,
-                                                     int rows_q, int rows_rem) {
-    constexpr int K = 2048 * T, G = 16 * T, KW = K / 8, NCH = K / 32, NIT = K / 8;
+                                                     int rows_q, int rows_rem, int Kr) {
+    static_assert(!(GLU && KR), "the GLU form takes K = 2048 T only");
+    constexpr int KM = 2048 * T, GM = 16 * T, NCHM = KM / 32, NITM = KM / 8;
     constexpr int RW = 2, WROWS = 16, NTHR = 512;
-    constexpr int XPT = (NIT + NTHR - 1) / NTHR;
-    constexpr int SPR = 2 * T, ZPR = 2 * T;                  // 16 B scale pieces, zero words per row
+    constexpr int XPT = (NITM + NTHR - 1) / NTHR;
+    constexpr int SPR = 2 * T, ZPRM = 2 * T;                 // 16 B scale pieces, zero words per row (LDS)
+    const int K = KR ? Kr : KM, G = KR ? Kr >> 7 : GM, KW = K / 8, NIT = K / 8;
+    const int ZPR = KR ? (G + 7) >> 3 : ZPRM;                // zero words per row in memory
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    float* xsum = reinterpret_cast<float*>(smem + NCH * 80);             // [NCH]
-    uint32_t* ssc = reinterpret_cast<uint32_t*>(xsum + NCH);             // [16 rows][G/2 words]
-    uint32_t* szr = ssc + WROWS * (G / 2);                               // [16 rows][2T words]
-    uint16_t* xraw = reinterpret_cast<uint16_t*>(szr + WROWS * ZPR);     // PERM: [K]
-    uint16_t* pl = xraw + K;                                             // PERM: [K]
+    float* xsum = reinterpret_cast<float*>(smem + NCHM * 80);            // [NCHM]
+    uint32_t* ssc = reinterpret_cast<uint32_t*>(xsum + NCHM);            // [16 rows][GM/2 words]
+    uint32_t* szr = ssc + WROWS * (GM / 2);                              // [16 rows][2T words]
+    uint16_t* xraw = reinterpret_cast<uint16_t*>(szr + WROWS * ZPRM);    // PERM: [KM]
+    uint16_t* pl = xraw + KM;                                            // PERM: [KM]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -601,10 +610,31 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         row = row < rend ? row : rend - 1;
         return GLU && (j & 1) ? row + N : row;
     };
-    if (sload) sv = load16(scales + (size_t)staged_row(tid / SPR) * G + (tid % SPR) * 8);
-    if (zload) {
-        const int j = tid - WROWS * SPR;
-        zv = qz[(size_t)staged_row(j / ZPR) * ZPR + j % ZPR];
+    // KR: word u of the [16][GM/2] scale block (row u / (GM/2), scale pair
+    // u % (GM/2)) and of the [16][2T] zero block; pairs past G/2 and words
+    // past ZPR stay 0
+    constexpr int KRS = KR ? (WROWS * (GM / 2) + NTHR - 1) / NTHR : 1;
+    constexpr int KRZ = KR && ZEROS ? (WROWS * ZPRM + NTHR - 1) / NTHR : 1;
+    uint32_t ksv[KRS], kzv[KRZ];
+    if (KR) {
+#pragma unroll
+        for (int i = 0; i < KRS; i++) {
+            const int u = tid + i * NTHR, row = u / (GM / 2), w = u % (GM / 2);
+            ksv[i] = u < WROWS * (GM / 2) && w < (G >> 1)
+                         ? *reinterpret_cast<const uint32_t*>(scales + (size_t)staged_row(row) * G + 2 * w)
+                         : 0u;
+        }
+#pragma unroll
+        for (int i = 0; i < KRZ; i++) {
+            const int u = tid + i * NTHR, row = u / ZPRM, w = u % ZPRM;
+            kzv[i] = ZEROS && u < WROWS * ZPRM && w < ZPR ? qz[(size_t)staged_row(row) * ZPR + w] : 0u;
+        }
+    } else {
+        if (sload) sv = load16(scales + (size_t)staged_row(tid / SPR) * G + (tid % SPR) * 8);
+        if (zload) {
+            const int j = tid - WROWS * SPR;
+            zv = qz[(size_t)staged_row(j / ZPR) * ZPR + j % ZPR];
+        }
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -622,15 +652,25 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         const uint32_t wrow = GLU ? (uint32_t)(n0 + r * N) : (uint32_t)(n0 + r);
 #pragma unroll
         for (int t = 0; t < T; t++) {
-            const uint32_t off = live ? wrow * (KW * 4) + (uint32_t)(64 * t + lane) * 16u : kNoRecord;
+            const bool in_k = !KR || 32 * (64 * t + lane) < K;
+            const uint32_t off = live && in_k ? wrow * (KW * 4) + (uint32_t)(64 * t + lane) * 16u : kNoRecord;
             wv[r][t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, off, 0, kNontemporal));
         }
     }
     asm volatile("" ::: "memory");
 
     // 3. staging
-    if (sload) *reinterpret_cast<u32x4*>(ssc + tid * 4) = sv;
-    if (zload) szr[tid - WROWS * SPR] = zv;
+    if (KR) {
+#pragma unroll
+        for (int i = 0; i < KRS; i++)
+            if (tid + i * NTHR < WROWS * (GM / 2)) ssc[tid + i * NTHR] = ksv[i];
+#pragma unroll
+        for (int i = 0; i < KRZ; i++)
+            if (ZEROS && tid + i * NTHR < WROWS * ZPRM) szr[tid + i * NTHR] = kzv[i];
+    } else {
+        if (sload) *reinterpret_cast<u32x4*>(ssc + tid * 4) = sv;
+        if (zload) szr[tid - WROWS * SPR] = zv;
+    }
     if (PERM) {
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
@@ -656,12 +696,14 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         }
     }
     // k-slot order {0,4,1,5 | 2,6,3,7} per 8 columns; chunk c (4 items) at c * 80 bytes;
-    // chunk sums over the 4 items held by 4 consecutive lanes
+    // chunk sums over the 4 items held by 4 consecutive lanes.  KR: the items
+    // past K (up to 2048 T) are staged as zeros.
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         const int it0 = tid + i * NTHR;
-        const bool live = it0 < NIT;
+        const bool live = it0 < (KR ? NITM : NIT);
         const int it = live ? it0 : NIT - 1;
+        if (KR && it0 >= NIT) xr[i] = u32x4{0u, 0u, 0u, 0u};
         u32x4 p;
         p[0] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x05040100u);
         p[1] = __builtin_amdgcn_perm(xr[i][2], xr[i][0], 0x07060302u);
@@ -702,9 +744,9 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
 #pragma unroll
         for (int t = 0; t < T; t++) {
             const int g = 16 * t + (lane >> 2);                 // group of chunk 64 t + lane
-            const uint32_t sw = ssc[wr * (G / 2) + (g >> 1)];
+            const uint32_t sw = ssc[wr * (GM / 2) + (g >> 1)];
             const float s = f16_dev((uint16_t)((g & 1) ? (sw >> 16) : (sw & 0xFFFFu)));
-            const uint32_t z = ZEROS ? (szr[wr * ZPR + (g >> 3)] >> (4 * (g & 7))) & 15u : 8u;
+            const uint32_t z = ZEROS ? (szr[wr * ZPRM + (g >> 3)] >> (4 * (g & 7))) & 15u : 8u;
             sc[r][t] = s;
             corr[r] = fmaf(s * (float)(128u + z), X[t], corr[r]);
         }
@@ -947,7 +989,8 @@ int launch_small_m(const W4Launch& a) {
     return launch_small_vs<XPT, MM, false, PERM>(a);
 }
 
-// k_w4a16_gemv1 applies: M = 1, group 128, K = 2048 T (T <= 8), 16-byte aligned scales.
+// LDS of k_w4a16_gemv1 for K = 2048 T (the ragged form takes that of the
+// next multiple of 2048).
 size_t gemv1_lds(size_t K, bool perm) {
     const size_t nch = K / 32, g = K / 128;
     return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
@@ -964,16 +1007,16 @@ unsigned gemv1_grid(int N, int per = 16) {
     return (unsigned)(nwg < N ? nwg : N);
 }
 
-template <int T, bool PERM>
+template <int T, bool PERM, bool KR>
 int launch_gemv1_t(const W4Launch& a) {
     dim3 grid(gemv1_grid(a.N)), block(512);
-    const size_t lds = gemv1_lds((size_t)a.K, PERM);
+    const size_t lds = gemv1_lds((size_t)(2048 * T), PERM);
     if (lds > 64 * 1024) {   // PERM at K > 8192: the staged copies of x and perm
         static std::atomic<uint64_t> lds_done[4];   // (zeros, f32 out) variants, per device
-        const void* kfn[4] = {reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, false, PERM>),
-                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, true, PERM>),
-                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, false, PERM>),
-                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, true, PERM>)};
+        const void* kfn[4] = {reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, false, PERM, false, KR>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, true, PERM, false, KR>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, false, PERM, false, KR>),
+                              reinterpret_cast<const void*>(&k_w4a16_gemv1<T, true, true, PERM, false, KR>)};
         const int v = (a.qz ? 2 : 0) + (a.y_f32 ? 1 : 0);
         if (snx::lds_optin(kfn[v], (int)lds, lds_done[v]) != hipSuccess) {
             snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
@@ -981,9 +1024,8 @@ int launch_gemv1_t(const W4Launch& a) {
         }
     }
 #define SNX_G1(Z, F)                                                                      \
-    k_w4a16_gemv1<T, Z, F, PERM><<<grid, block, lds, a.s>>>(a.x, a.qw, a.scales, a.qz, a.perm, \
-                                                            a.y, a.bias, a.N, a.N / (int)grid.x, \
-                                                            a.N % (int)grid.x)
+    k_w4a16_gemv1<T, Z, F, PERM, false, KR><<<grid, block, lds, a.s>>>(                           \
+        a.x, a.qw, a.scales, a.qz, a.perm, a.y, a.bias, a.N, a.N / (int)grid.x, a.N % (int)grid.x, a.K)
     if (a.qz) {
         if (a.y_f32) SNX_G1(true, true);
         else SNX_G1(true, false);
@@ -995,24 +1037,34 @@ int launch_gemv1_t(const W4Launch& a) {
     return snx_launch_check("k_w4a16_gemv1");
 }
 
+// k_w4a16_gemv1 applies: M = 1, group 128, K a multiple of 256 up to 16384;
+// K = 2048 T takes 16-byte aligned scales, the ragged form (other K) 4-byte
+// aligned ones; 4-byte aligned zero words; weight offsets below the buffer
+// limit.
 bool gemv1_ok(const W4Launch& a) {
-    return a.M == 1 && a.group == 128 && a.K % 2048 == 0 && a.K <= 16384 &&
-           ((uintptr_t)a.scales & 15u) == 0 && ((uintptr_t)a.qz & 3u) == 0 &&
+    const uintptr_t salign = a.K % 2048 == 0 ? 15u : 3u;
+    return a.M == 1 && a.group == 128 && a.K % 256 == 0 && a.K >= 256 && a.K <= 16384 &&
+           ((uintptr_t)a.scales & salign) == 0 && ((uintptr_t)a.qz & 3u) == 0 &&
            (uint64_t)a.N * (uint64_t)a.K / 2 < kNoRecord;   // buffer offsets of the weights
+}
+
+template <bool PERM, bool KR>
+int launch_gemv1_k(const W4Launch& a) {
+    switch ((a.K + 2047) / 2048) {
+        case 1: return launch_gemv1_t<1, PERM, KR>(a);
+        case 2: return launch_gemv1_t<2, PERM, KR>(a);
+        case 3: return launch_gemv1_t<3, PERM, KR>(a);
+        case 4: return launch_gemv1_t<4, PERM, KR>(a);
+        case 5: return launch_gemv1_t<5, PERM, KR>(a);
+        case 6: return launch_gemv1_t<6, PERM, KR>(a);
+        case 7: return launch_gemv1_t<7, PERM, KR>(a);
+        default: return launch_gemv1_t<8, PERM, KR>(a);
+    }
 }
 
 template <bool PERM>
 int launch_gemv1(const W4Launch& a) {
-    switch (a.K / 2048) {
-        case 1: return launch_gemv1_t<1, PERM>(a);
-        case 2: return launch_gemv1_t<2, PERM>(a);
-        case 3: return launch_gemv1_t<3, PERM>(a);
-        case 4: return launch_gemv1_t<4, PERM>(a);
-        case 5: return launch_gemv1_t<5, PERM>(a);
-        case 6: return launch_gemv1_t<6, PERM>(a);
-        case 7: return launch_gemv1_t<7, PERM>(a);
-        default: return launch_gemv1_t<8, PERM>(a);
-    }
+    return a.K % 2048 == 0 ? launch_gemv1_k<PERM, false>(a) : launch_gemv1_k<PERM, true>(a);
 }
 
 template <int T>
@@ -1021,7 +1073,7 @@ int launch_gemv1_glu_t(const W4Launch& a) {
     const size_t lds = gemv1_lds((size_t)a.K, false);
 #define SNX_G1(Z)                                                                                 \
     k_w4a16_gemv1<T, Z, false, false, true><<<grid, block, lds, a.s>>>(                           \
-        a.x, a.qw, a.scales, a.qz, nullptr, a.y, a.bias, a.N, a.N / (int)grid.x, a.N % (int)grid.x)
+        a.x, a.qw, a.scales, a.qz, nullptr, a.y, a.bias, a.N, a.N / (int)grid.x, a.N % (int)grid.x, a.K)
     if (a.qz) SNX_G1(true);
     else SNX_G1(false);
 #undef SNX_G1
@@ -1502,8 +1554,8 @@ size_t snx_w4a16_small_lds(size_t M, size_t K, int perm) {
     return lds;
 }
 
-// The streaming M = 1 kernel: group 128, K = 2048 T up to 16384, scales
-// 16-byte and qzeros 4-byte aligned.
+// The streaming M = 1 kernel: group 128, K a multiple of 256 up to 16384,
+// scales 16-byte (K = 2048 T) or 4-byte (other K) and qzeros 4-byte aligned.
 int snx_w4a16_gemv1_ok(size_t M, size_t K, int group, const void* scales, const void* qzeros) {
     W4Launch a{};
     a.M = (int)M;
@@ -1524,7 +1576,7 @@ int snx_w4a16_small_ok(size_t M, size_t K, int group, int perm) {
 // The GLU form of the M = 1 kernel applies: its shapes, with the stacked
 // [2F][K] weights within the buffer offsets.
 int snx_w4a16_gemv1_swiglu_ok(size_t F, size_t K, int group, const void* scales, const void* qzeros) {
-    return F && snx_w4a16_gemv1_ok(1, K, group, scales, qzeros) && (uint64_t)F * K < kNoRecord;
+    return F && K % 2048 == 0 && snx_w4a16_gemv1_ok(1, K, group, scales, qzeros) && (uint64_t)F * K < kNoRecord;
 }
 
 // M = 1 gate/up projection with the SwiGLU step (the GLU form of the M = 1

@@ -24,6 +24,12 @@ int check(hipError_t e, const char* what) {
 }
 
 hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// zero fill of a new zeroed workspace (a kernel, not a memset, so that a
+// caller capturing the stream into a graph records an ordinary kernel node)
+__global__ void __launch_bounds__(256) k_fill_zero_u32(uint32_t* __restrict__ p, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
 }  // namespace
 
 extern "C" {
@@ -115,7 +121,8 @@ int thread_key() {
 }
 }  // namespace
 
-void* snx_workspace(size_t bytes, int slot, void* stream) {
+namespace {
+void* workspace(size_t bytes, int slot, void* stream, bool zeroed) {
     int dev = 0;
     if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
     if (bytes == 0) bytes = 1;
@@ -128,6 +135,14 @@ void* snx_workspace(size_t bytes, int slot, void* stream) {
     const size_t want = (bytes + (bytes >> 2) + 4095) & ~(size_t)4095;   // +25% headroom
     void* p = nullptr;
     if (snx_hip_malloc_async(&p, want, stream)) return nullptr;
+    if (zeroed) {
+        k_fill_zero_u32<<<(unsigned)(want / 4 / 256 < 1024 ? (want / 4 + 255) / 256 : 1024), 256, 0, S(stream)>>>(
+            static_cast<uint32_t*>(p), want / 4);
+        if (snx_launch_check("k_fill_zero_u32")) {
+            (void)snx_hip_free_async(p, stream);
+            return nullptr;
+        }
+    }
     if (w) {
         if (snx_hip_free_async(w->ptr, stream)) return nullptr;
         w->ptr = p;
@@ -137,6 +152,14 @@ void* snx_workspace(size_t bytes, int slot, void* stream) {
     }
     return p;
 }
+}  // namespace
+
+void* snx_workspace(size_t bytes, int slot, void* stream) { return workspace(bytes, slot, stream, false); }
+
+// As snx_workspace, with a new buffer zero-filled (stream-ordered) when it is
+// taken; for data the caller's kernels return to zero before they end (the
+// split GEMM's arrival counters).
+void* snx_workspace_zeroed(size_t bytes, int slot, void* stream) { return workspace(bytes, slot, stream, true); }
 
 // Frees (stream-ordered) every workspace of this thread on `stream`, for a
 // caller about to destroy that stream.

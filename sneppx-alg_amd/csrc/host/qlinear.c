@@ -172,6 +172,10 @@ static int w4a16_linear(const char* who, int noalloc, const uint16_t* x, const u
         if (!rc) rc = snx_k_w4a16_reduce(part, y, y_f32, (int)S, M * N, N, bias, stream);
         return rc;
     }
+    if (!g_idx && M == 1 && aligned16(x) && aligned16(qweight) &&
+        snx_w4a16_gemv1_ok(1, K, group, scales, qzeros))
+        /* the streaming M = 1 kernel (K a multiple of 256 up to 16384) */
+        return snx_k_w4a16_gemv(x, qweight, scales, qzeros, NULL, y, bias, y_f32, 1, N, K, group, stream);
     if (!g_idx && aligned16(x) && aligned16(qweight) &&
         snx_w4a16_gemv_supported(M < 64 ? M : 64, N, K, group)) {
         /* decode GEMV; larger M in 64-row slices that reuse each weight load */

@@ -19,6 +19,8 @@ void snx_set_error(const char* fmt, ...);
  * the calling host thread; slot 1 is for a call made from inside another
  * one.  NULL on failure. */
 void* snx_workspace(size_t bytes, int slot, void* stream);
+/* as snx_workspace; a newly taken buffer is zero-filled on `stream` first */
+void* snx_workspace_zeroed(size_t bytes, int slot, void* stream);
 /* stream-ordered release of the calling thread's workspaces on `stream` */
 void snx_release_workspaces(void* stream);
 /* the current device's static scratch array (noalloc.hip) when `bytes` fit

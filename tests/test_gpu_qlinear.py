@@ -203,6 +203,58 @@ def test_w4a16_gemv_m1_group128(lib, oracle, N, K, sym, out):
     assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
 
 
+@pytest.mark.parametrize("N,K,sym,out,bias,soff", [
+    (4096, 1792, False, "bf16", False, 0), (4096, 1792, True, "f32", True, 2), (17, 256, False, "f32", False, 2),
+    (4096, 512, False, "f32", True, 0), (1001, 2304, True, "bf16", False, 2), (4096, 3584, False, "f32", False, 0),
+    (300, 7168, False, "f32", True, 2), (16, 10496, True, "bf16", False, 0), (33, 16128, False, "f32", False, 2)])
+def test_w4a16_gemv_m1_ragged_k(lib, oracle, N, K, sym, out, bias, soff):
+    # the M = 1 kernel's ragged form: K a multiple of 256 but not of 2048
+    # (the down / O projections of a tensor-parallel shard: 4096 x 1792 and
+    # 4096 x 512 at TP = 8, 4096 x 3584 at TP = 4, 4096 x 7168 at TP = 2),
+    # group scales that are 4-byte but not 16-byte aligned (soff = 2 fp16
+    # values into the buffer), with and without zero points and a bias
+    group = 128
+    print(f"[gpu] w4a16 gemv M=1 ragged N={N} K={K} sym={sym} out={out} bias={bias} soff={soff}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, 3 * N + K, sym=sym)
+    x = bf16_bits(np.random.default_rng(K + 1).normal(0, 1, (1, K)).astype(np.float32))
+    b = np.random.default_rng(K + 2).normal(0, 1, N).astype(np.float32) if bias else None
+    scb = torch.zeros(N * G + soff, dtype=torch.int16, device=DEV)
+    scb[soff:] = to_dev(sc.view(np.int16).reshape(-1))
+    sc_d = scb[soff:].view(N, G)
+    assert sc_d.data_ptr() % 16 == (4 * (soff // 2)) % 16
+    y = torch.empty((1, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), sc_d, None if sym else to_dev(qz), None, G, y, group,
+                      bias=None if b is None else to_dev(b))
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, None if sym else qz, None, N, K, group)
+    if b is not None:
+        yo = oracle.add_bias(yo, b)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+
+
+@pytest.mark.parametrize("K,zeros", [(1792, False), (3584, True), (512, True)])
+def test_w4a16_actorder_prepared_ragged_k(lib, oracle, K, zeros):
+    """Act-order weights at the row-parallel shard widths (K not a multiple
+    of 2048) through the M = 1 kernel's ragged form with the activation
+    gather, against the oracle on the original column order."""
+    N = 1040
+    print(f"[gpu] w4a16 act-order M=1 ragged K={K} zeros={zeros}", flush=True)
+    rng = np.random.default_rng(K)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 29, g_idx=g_idx)
+    qz = rng.integers(0, 2**32, (N, (G + 7) // 8), dtype=np.uint64).astype(np.uint32) if zeros else None
+    x = bf16_bits(rng.normal(0, 1, (1, K)).astype(np.float32))
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), G, qs, perm)
+    y = torch.empty((1, N), dtype=torch.float32, device=DEV)
+    lib.qlinear_w4a16_actorder(to_dev(x), qs, to_dev(sc), None if qz is None else to_dev(qz), perm, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, g_idx, N, K, 128)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
 @pytest.mark.parametrize("M,N,K,sym,out", [
     (2, 8197, 1024, False, "f32"), (3, 45, 2048, True, "bf16"), (5, 4099, 3072, False, "f32"),
     (8, 11008, 4096, True, "f32"), (16, 300, 4096, False, "bf16"), (16, 9000, 2048, True, "f32"),
@@ -595,6 +647,72 @@ def test_w8a8_fp8_ragged_multi_tile(lib, oracle, M, N, K):
         assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], ref) <= TOL_BF16, (m0, n0)
 
 
+@pytest.mark.parametrize("kind,N,bias", [("i8", 1792, False), ("fp8", 1792, True), ("i8", 3584, True),
+                                         ("fp8", 3584, False)])
+def test_w8a8_tensor_parallel_shard_split_k(lib, oracle, kind, N, bias):
+    """C4 on one GPU's column shard of a tensor-parallel layer: at N = 14336
+    / 8 the 64 tiles fill a quarter of the CUs, so the persistent kernel
+    splits K into 2 spans and the last-arriving wave of each (tile, wave)
+    adds the spans' partial sums in span order; N = 14336 / 4 (128 tiles)
+    runs unsplit.  Sampled 64x64 sub-tiles and the
+    corners against the oracle (int8 accumulators bit-exact); a call of
+    another split shape in between, then a repeat giving bit-identical
+    output (the arrival counters return to 0; the sums' order does not
+    depend on which wave arrives last)."""
+    M, K = 2048, 4096
+    print(f"[gpu] w8a8 {kind} shard {M}x{N}x{K} bias={bias}", flush=True)
+    rng = np.random.default_rng(N + (7 if kind == "fp8" else 0))
+    b = rng.normal(0, 1, N).astype(np.float32) if bias else None
+    bd = None if b is None else to_dev(b)
+    g = torch.Generator(device=DEV).manual_seed(N)
+    a32 = torch.randn((M, K), device=DEV, generator=g)
+    w32 = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    fp8 = kind == "fp8"
+    A = torch.empty((M, K), dtype=torch.uint8 if fp8 else torch.int8, device=DEV)
+    W = torch.empty((N, K), dtype=torch.uint8 if fp8 else torch.int8, device=DEV)
+    if fp8:
+        sA, sW = torch.empty(1, device=DEV), torch.empty(1, device=DEV)
+        lib.dev_quantize_fp8_e4m3_scaled(a32, A, sA)
+        lib.dev_quantize_fp8_e4m3_scaled(w32, W, sW)
+        run = lambda o, A_=A, W_=W, sA_=sA, sW_=sW: lib.qlinear_w8a8_fp8(A_, sA_, W_, sW_, o, bias=bd)  # noqa: E731
+    else:
+        sA, sW = torch.empty(M, device=DEV), torch.empty(N, device=DEV)
+        lib.dev_quantize_int8_channel(a32, A, sA)
+        lib.dev_quantize_int8_channel(w32, W, sW)
+        run = lambda o, A_=A, W_=W, sA_=sA, sW_=sW: lib.qlinear_w8a8_i8(A_, sA_, W_, sW_, o, bias=bd)  # noqa: E731
+    del a32, w32
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    run(out)
+    # another split shape on the same stream (10 tiles), then a repeat
+    small = torch.empty((300, 1000), dtype=torch.bfloat16, device=DEV)
+    if fp8:
+        lib.qlinear_w8a8_fp8(A[:300, :1024].contiguous(), sA, W[:1000, :1024].contiguous(), sW, small)
+    else:
+        lib.qlinear_w8a8_i8(A[:300, :1024].contiguous(), sA[:300].contiguous(), W[:1000, :1024].contiguous(),
+                            sW[:1000].contiguous(), small)
+    again = torch.empty_like(out)
+    run(again)
+    Cm = None
+    if not fp8:
+        Cm = torch.empty((M, N), dtype=torch.int32, device=DEV)
+        lib.qlinear_i8_gemm_i32(A, W, Cm)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), again.view(torch.int16))
+    An, Wn, outn = A.cpu().numpy(), W.cpu().numpy(), bf16_to_f32(u16(out))
+    blocks = [(0, 0), (M - 64, N - 64), (M - 64, 0), (0, N - 64)]
+    blocks += [(int(rng.integers(0, M - 64)), int(rng.integers(0, N - 64))) for _ in range(4)]
+    for m0, n0 in blocks:
+        if fp8:
+            ref = oracle.fp8_gemm(An[m0:m0 + 64], Wn[n0:n0 + 64], np.float32(sA.item()), np.float32(sW.item()))
+        else:
+            acc = oracle.i8_gemm_i32(An[m0:m0 + 64], Wn[n0:n0 + 64])
+            assert np.array_equal(Cm.cpu().numpy()[m0:m0 + 64, n0:n0 + 64], acc), (m0, n0)
+            ref = oracle.w8a8_epilogue(acc, sA.cpu().numpy()[m0:m0 + 64], sW.cpu().numpy()[n0:n0 + 64])
+        if b is not None:
+            ref = oracle.add_bias(ref, b[n0:n0 + 64])
+        assert rel_err(outn[m0:m0 + 64, n0:n0 + 64], ref) <= TOL_BF16, (m0, n0)
+
+
 def _random_qzeros(rng, N, G):
     z = rng.integers(0, 16, (N, ((G + 7) // 8) * 8)).astype(np.uint32)
     z[:, G:] = 0
@@ -717,29 +835,32 @@ def test_w4a16_subnormal_fp16_scales(lib, oracle, M, K, group):
     assert rel_err(got[:, ::3], yo[:, ::3]) <= TOL_F32
 
 
-def test_decode_token_through_llama3_layer_linears(lib, oracle):
+@pytest.mark.parametrize("tp", [1, 8])
+def test_decode_token_through_llama3_layer_linears(lib, oracle, tp):
     """One token (M = 1) through the four linears of a Llama-3-8B layer as the
-    bench's decode line runs them (QKV 6144x4096, O 4096x4096 on the first
+    bench's decode lines run them (QKV 6144x4096, O 4096x4096 on the first
     4096 QKV outputs, gate/up + SwiGLU 2x14336x4096 in one launch, down
-    4096x14336), each stage against the oracle fed the same bf16 input."""
-    print("[gpu] decode token through the Llama-3-8B layer linears", flush=True)
-    H, F = 4096, 14336
+    4096x14336), or one GPU's shard of them at tp = 8 (QKV 768x4096, O
+    4096x512, gate/up 2x1792x4096, down 4096x1792), each stage against the
+    oracle fed the same bf16 input."""
+    print(f"[gpu] decode token through the Llama-3-8B layer linears tp={tp}", flush=True)
+    H, F, QKV, A = 4096, 14336 // tp, 6144 // tp, 4096 // tp
     rng = np.random.default_rng(77)
     w = {n: _w4_case(oracle, N, K, 128, 80 + i)
-         for i, (n, N, K) in enumerate((("qkv", 6144, H), ("o", H, H), ("gu", 2 * F, H), ("down", H, F)))}
+         for i, (n, N, K) in enumerate((("qkv", QKV, H), ("o", H, A), ("gu", 2 * F, H), ("down", H, F)))}
     x = bf16_bits(rng.normal(0, 1, (1, H)).astype(np.float32))
     dev = {n: tuple(to_dev(a) for a in v[:3]) for n, v in w.items()}
-    qkv = torch.empty((1, 6144), dtype=torch.bfloat16, device=DEV)
+    qkv = torch.empty((1, QKV), dtype=torch.bfloat16, device=DEV)
     o = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
     h = torch.empty((1, F), dtype=torch.bfloat16, device=DEV)
     y = torch.empty((1, H), dtype=torch.bfloat16, device=DEV)
     lib.qlinear_w4a16(to_dev(x), *dev["qkv"], None, H // 128, qkv, 128)
-    lib.qlinear_w4a16(qkv[:, :H], *dev["o"], None, H // 128, o, 128)       # the first 4096 values
+    lib.qlinear_w4a16(qkv[:, :A], *dev["o"], None, A // 128, o, 128)       # the first A values
     lib.qlinear_w4a16_swiglu(o, *dev["gu"], h, 128)
     lib.qlinear_w4a16(h, *dev["down"], None, F // 128, y, 128)
     torch.cuda.synchronize()
     # each stage against the oracle on the GPU's own (bf16) input to it
-    steps = (("qkv", x, qkv, 6144, H), ("o", u16(qkv)[:, :H], o, H, H), ("down", u16(h), y, H, F))
+    steps = (("qkv", x, qkv, QKV, H), ("o", u16(qkv)[:, :A], o, H, A), ("down", u16(h), y, H, F))
     for name, inp, got, N, K in steps:
         qw, sc, qz, _ = w[name]
         rc, want = oracle.w4a16_linear(np.ascontiguousarray(inp), qw, sc, qz, None, N, K, 128)
