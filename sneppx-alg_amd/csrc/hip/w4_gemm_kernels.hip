@@ -115,7 +115,16 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // column n0 + c, column c >= 128 the up column F + n0 + c - 128 of the same
 // output column, so waves 0-3 hold gate values and waves 4-7 the matching up
 // values; the epilogue pairs them through LDS.
-template <bool ZEROS, bool YF32, int WN, bool SWIGLU>
+// SPLIT > 1 (too few tiles to fill the CUs, such as the QKV projection of one
+// GPU's tensor-parallel shard): workgroup unit v covers tile v % ntiles and
+// the K steps of span v / ntiles (K / SPLIT columns).  Each wave stores its
+// span's fp32 results to its slot of `part` (system-coherent policy, so no
+// L2 keeps a copy another XCD cannot see), waits until they are written and
+// counts itself in cnt[tile][wave]; the last of the SPLIT waves of a
+// (tile, wave) adds the slots in span order (the same fp32 sums whichever
+// wave is last), returns the counter to 0 and writes the output.  No wave
+// waits for another.
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU, int SPLIT = 1>
 __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
                                                     const float* __restrict__ xs,
                                                     const uint32_t* __restrict__ qw,
@@ -123,7 +132,9 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                                                     const uint32_t* __restrict__ qz,
                                                     void* __restrict__ y,
                                                     const float* __restrict__ bias, int M, int N,
-                                                    int K, int G, int gshift, int Mp, int tiles_m) {
+                                                    int K, int G, int gshift, int Mp, int tiles_m,
+                                                    u32x4* __restrict__ part, uint32_t* __restrict__ cnt) {
+    static_assert(SPLIT == 1 || !SWIGLU, "the SwiGLU epilogue takes whole-K tiles");
     // WN waves along N, 8 / WN along M: each wave owns RW rows x CW columns,
     // FM x FN blocks of 32 x 32; the result sits in FM / 2 x FN pairs of
     // blocks stacked along M (the 2-block f32 MFMA's output)
@@ -136,9 +147,11 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     const int wm = wave / WN, wn = wave % WN;
     const int r32 = lane & 31, h = lane >> 5;
 
-    // XCD-aware order: consecutive tiles of one M-row of tiles share an XCD
+    // XCD-aware order: consecutive units of one M-row of tiles share an XCD
     const int b = blockIdx.x, nb = gridDim.x;
-    const int tile = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int unit = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    const int ntiles = nb / SPLIT;
+    const int tile = SPLIT == 1 ? unit : unit % ntiles, span = SPLIT == 1 ? 0 : unit / ntiles;
     const int tm = tile % tiles_m, tn = tile / tiles_m;
     const int m0 = tm * GBM, n0 = tn * (SWIGLU ? GBN / 2 : GBN);
     // weight row of tile column c (clamped into the matrix)
@@ -223,7 +236,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
 
-    const int nk = K / GBK;
+    const int nk = K / GBK / SPLIT, kb = span * nk;   // this unit's K steps: kb .. kb + nk - 1
     // activation fragment: row wm RW + 32 i + r32, logical chunk 2 s + h
     // (rows 16 apart share the swizzle, so row & 15 = r32 & 15)
     const uint8_t* arow = lds + (wm * RW + r32) * (GBK * 2);
@@ -256,18 +269,18 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     uint32_t sr[FN], zr[FN];
     float xr[QM];
     f32x16 acc[FM][FN];
-    dload(0, 0);
-    dload(1, nk > 1 ? 1 : 0);
-    for (int kt = 0; kt < nk; kt++) {
-        const int cur = kt % GSTAGES;
+    dload(0, kb);
+    dload(1, kb + (nk > 1 ? 1 : 0));
+    for (int kt = kb; kt < kb + nk; kt++) {
+        const int cur = (kt - kb) % GSTAGES;
         // vmcnt(8): stage kt landed, kt + 1 may fly; lgkmcnt(0): this wave is
         // done with stage kt - 1.  A raw barrier: a __syncthreads() fence would
         // wait for stage kt + 1 as well.
         __builtin_amdgcn_s_waitcnt(0x0078);
         __builtin_amdgcn_s_barrier();
         __builtin_amdgcn_sched_barrier(0);    // nothing below moves above the wait
-        const int kn = kt + 2 < nk ? kt + 2 : nk - 1;   // past the end: reload, unused
-        const int nbuf = (kt + 2) % GSTAGES;
+        const int kn = kt + 2 < kb + nk ? kt + 2 : kb + nk - 1;   // past the end: reload, unused
+        const int nbuf = (kt - kb + 2) % GSTAGES;
 
         const uint8_t* ab = arow + cur * GRING;
         u32x4 wv[FN][2];
@@ -317,6 +330,78 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
         fold(acc, xr, sr, zr, (kt * GBK) >> gshift);
     }
     __builtin_amdgcn_s_waitcnt(0x0070);   // the ring's last (unused) loads drain before exit
+
+    if constexpr (SPLIT > 1) {
+        // slot (unit, wave): QM x FN results x 8 pieces of 16 B per lane, lane-major
+        constexpr int NP = QM * FN * 8, SLOTB = NP * 64 * 16;
+        constexpr int kSysCoherent = 1 | 16;          // buffer cache policy sc0 sc1
+        const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)part, (short)0, nb * 8 * SLOTB, 0x00020000);
+        const uint32_t mine = (uint32_t)((span * ntiles + tile) * 8 + wave) * SLOTB;
+#pragma unroll
+        for (int i = 0; i < QM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int p = 0; p < 8; p++) {
+                    // elements copied to scalars first: a bit cast of a vector
+                    // element operand reads the wrong element with this compiler
+                    const float f0 = yq[i][j][4 * p], f1 = yq[i][j][4 * p + 1];
+                    const float f2 = yq[i][j][4 * p + 2], f3 = yq[i][j][4 * p + 3];
+                    const u32x4 v = {__builtin_bit_cast(uint32_t, f0), __builtin_bit_cast(uint32_t, f1),
+                                     __builtin_bit_cast(uint32_t, f2), __builtin_bit_cast(uint32_t, f3)};
+                    __builtin_amdgcn_raw_buffer_store_b128(v, rp, lane * 16,
+                                                           mine + ((i * FN + j) * 8 + p) * 1024, kSysCoherent);
+                }
+        // the slot is written before it is counted, and no result register is
+        // written before the stores have read it (a 16-byte store reads its
+        // data after issue): nothing below moves above this wait
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0f70);           // vmcnt(0)
+        __builtin_amdgcn_sched_barrier(0);
+        uint32_t c = 0;
+        if (lane == 0) c = atomicAdd(&cnt[tile * 8 + wave], 1u);
+        if (__builtin_amdgcn_readfirstlane(c) != SPLIT - 1) return;
+        // the last wave of this (tile, wave): the spans' slots in span order, in
+        // chunks of 4 pieces x SPLIT spans, each chunk's offsets carrying a zero
+        // the previous chunk's sums produce (so the loads cannot all be hoisted)
+        const uint32_t first = (uint32_t)(tile * 8 + wave) * SLOTB, sstride = (uint32_t)ntiles * 8 * SLOTB;
+        uint32_t dep = 0;
+#pragma unroll
+        for (int i = 0; i < QM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int p0 = 0; p0 < 8; p0 += 4) {
+                    u32x4 v[SPLIT][4];
+#pragma unroll
+                    for (int s2 = 0; s2 < SPLIT; s2++)
+#pragma unroll
+                        for (int pp = 0; pp < 4; pp++)
+                            v[s2][pp] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                rp, lane * 16, first + dep + s2 * sstride + ((i * FN + j) * 8 + p0 + pp) * 1024,
+                                kSysCoherent));
+#pragma unroll
+                    for (int pp = 0; pp < 4; pp++)
+#pragma unroll
+                        for (int e = 0; e < 4; e++) {
+                            const uint32_t w0 = v[0][pp][e];
+                            float r = __builtin_bit_cast(float, w0);
+#pragma unroll
+                            for (int s2 = 1; s2 < SPLIT; s2++) {
+                                const uint32_t w = v[s2][pp][e];
+                                r += __builtin_bit_cast(float, w);
+                            }
+                            yq[i][j][4 * (p0 + pp) + e] = r;
+                        }
+                    const f32x16 ch = __builtin_shufflevector(yq[i][j], yq[i][j], 0, 1, 2, 3, 4, 5, 6, 7, 8, 9,
+                                                              10, 11, 12, 13, 14, 15);
+                    const f32x16 cl = __builtin_shufflevector(yq[i][j], yq[i][j], 16, 17, 18, 19, 20, 21, 22, 23,
+                                                              24, 25, 26, 27, 28, 29, 30, 31);
+                    asm volatile("s_mov_b32 %0, 0" : "=s"(dep) : "v"(p0 == 0 ? ch : cl));
+                }
+        if (lane == 0) atomicExch(&cnt[tile * 8 + wave], 0u);   // ready for the next call
+    }
 
     if constexpr (SWIGLU) {
         static_assert(WN == 8 && FN == 1 && RW == GBM, "SwiGLU pairs wave w with wave w + 4");
@@ -379,23 +464,40 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     }
 }
 
-template <bool ZEROS, bool YF32, int WN, bool SWIGLU>
-int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
-                   const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
-                   int N, int K, int group, int Mp, hipStream_t st) {
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU, int SPLIT>
+int launch_w4_gemm_s(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                     const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
+                     int N, int K, int group, int Mp, void* part, uint32_t* cnt, hipStream_t st) {
     const int tn_cols = SWIGLU ? GBN / 2 : GBN;
     const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + tn_cols - 1) / tn_cols;
     const size_t lds = (size_t)GSTAGES * GRING;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU>);
+    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU, SPLIT>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
     const int gshift = __builtin_ctz((unsigned)group);
-    k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU><<<tiles_m * tiles_n, 512, lds, st>>>(
-        xp, xs, qw, scales, qz, y, bias, M, N, K, K / group, gshift, Mp, tiles_m);
+    k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU, SPLIT><<<tiles_m * tiles_n * SPLIT, 512, lds, st>>>(
+        xp, xs, qw, scales, qz, y, bias, M, N, K, K / group, gshift, Mp, tiles_m,
+        static_cast<u32x4*>(part), cnt);
     return snx_launch_check("k_w4a16_gemm");
+}
+
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU>
+int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                   const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
+                   int N, int K, int group, int Mp, int split, void* part, uint32_t* cnt, hipStream_t st) {
+    if constexpr (!SWIGLU) {
+        if (split == 4)
+            return launch_w4_gemm_s<ZEROS, YF32, WN, false, 4>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
+                                                               part, cnt, st);
+        if (split == 2)
+            return launch_w4_gemm_s<ZEROS, YF32, WN, false, 2>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
+                                                               part, cnt, st);
+    }
+    return launch_w4_gemm_s<ZEROS, YF32, WN, SWIGLU, 1>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
+                                                         nullptr, nullptr, st);
 }
 
 // SiLU(gate) * up between the gate/up and down projections of a SwiGLU MLP:
@@ -548,16 +650,42 @@ int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t
     return snx_launch_check("k_w4_prep_x");
 }
 
+// K spans of the prefill GEMM for M x N x K (no SwiGLU step): 4 or 2 when
+// the tiles fill at most a quarter or a half of the CUs and each span keeps
+// at least two 128-column steps, else 1.
+int snx_w4a16_gemm_splits(size_t M, size_t N, size_t K) {
+    const size_t ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    const size_t ncu = (size_t)snx::cu_count(), nk = K / GBK;
+    if (ntiles * 4 <= ncu && nk % 4 == 0 && nk >= 8) return 4;
+    if (ntiles * 2 <= ncu && nk % 2 == 0 && nk >= 4) return 2;
+    return 1;
+}
+
+// Bytes of the span partials (`part`) and arrival counters (`cnt`) of a
+// `splits`-span call: a 16 KB slot per (unit, wave), a counter per (tile, wave).
+size_t snx_w4a16_gemm_part_bytes(size_t M, size_t N, int splits) {
+    const size_t ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    return ntiles * (size_t)splits * 8 * (2 * 8 * 64 * 16);
+}
+size_t snx_w4a16_gemm_cnt_bytes(size_t M, size_t N) {
+    return ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN) * 8 * sizeof(uint32_t);
+}
+
 int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      const uint16_t* scales, const uint32_t* qzeros, void* y, const float* bias,
-                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, void* st) {
+                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, int splits,
+                     void* part, uint32_t* cnt, void* st) {
     const int m = (int)M, n = (int)N, k = (int)K, mp = (int)Mp;
-    if (qzeros) {
-        if (y_f32) return launch_w4_gemm<true, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
-        return launch_w4_gemm<true, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+    if (splits > 1 && (!part || !cnt || splits != snx_w4a16_gemm_splits(M, N, K))) {
+        snx_set_error("w4a16 gemm: %d K spans need their partials and counters (and a shape that takes them)", splits);
+        return -1;
     }
-    if (y_f32) return launch_w4_gemm<false, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
-    return launch_w4_gemm<false, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, S(st));
+    if (qzeros) {
+        if (y_f32) return launch_w4_gemm<true, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
+        return launch_w4_gemm<true, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
+    }
+    if (y_f32) return launch_w4_gemm<false, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
+    return launch_w4_gemm<false, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
 }
 
 int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t* qw,
@@ -566,8 +694,10 @@ int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t*
                             void* st) {
     const int m = (int)M, f = (int)F, k = (int)K, mp = (int)Mp;
     if (qzeros)
-        return launch_w4_gemm<true, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, S(st));
-    return launch_w4_gemm<false, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, S(st));
+        return launch_w4_gemm<true, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, 1,
+                                                        nullptr, nullptr, S(st));
+    return launch_w4_gemm<false, false, W4_WN, true>(xp, xs, qw, scales, qzeros, out, bias, m, f, k, group, mp, 1,
+                                                     nullptr, nullptr, S(st));
 }
 
 }  // extern "C"

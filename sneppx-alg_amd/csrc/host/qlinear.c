@@ -150,9 +150,19 @@ static int w4a16_linear(const char* who, int noalloc, const uint16_t* x, const u
         if (!ws) return -1;
         uint16_t* xp = (uint16_t*)ws;
         float* xs = (float*)(ws + xp_bytes);
+        /* with few tiles, K in spans (partials in a workspace; not for the
+         * allocation-free entry point) */
+        const int splits = noalloc ? 1 : snx_w4a16_gemm_splits(M, N, K);
+        void* part = NULL;
+        uint32_t* cnt = NULL;
+        if (splits > 1) {
+            part = snx_workspace(snx_w4a16_gemm_part_bytes(M, N, splits), 3, stream);
+            cnt = (uint32_t*)snx_workspace_zeroed(snx_w4a16_gemm_cnt_bytes(M, N), 4, stream);
+            if (!part || !cnt) return -1;
+        }
         int rc = snx_k_w4_prep_x(x, xp, xs, M, K, Mp, stream);
         if (!rc) rc = snx_k_w4a16_gemm(xp, xs, qweight, scales, qzeros, y, bias, y_f32, M, N, K,
-                                       group, Mp, stream);
+                                       group, Mp, splits, part, cnt, stream);
         return rc;
     }
     if (!g_idx && snx_w4a16_mt_ok(M, K, group, 0) && aligned16(x) && aligned16(qweight) &&

@@ -170,9 +170,16 @@ size_t snx_w4_prep_rows(size_t M);
 int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group);
 int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,
                     void* stream);
+/* K spans the GEMM splits M x N x K into (1, 2 or 4: with few tiles), and
+ * the partials / counters workspaces a call with `splits` > 1 takes (the
+ * counters zero when taken; every call leaves them zero) */
+int snx_w4a16_gemm_splits(size_t M, size_t N, size_t K);
+size_t snx_w4a16_gemm_part_bytes(size_t M, size_t N, int splits);
+size_t snx_w4a16_gemm_cnt_bytes(size_t M, size_t N);
 int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      const uint16_t* scales, const uint32_t* qzeros, void* y, const float* bias,
-                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, void* stream);
+                     int y_f32, size_t M, size_t N, size_t K, int group, size_t Mp, int splits,
+                     void* part, uint32_t* cnt, void* stream);
 
 /* SwiGLU step: out [T][F] = bf16(silu(gu[:, :F]) * gu[:, F:]), F % 8 == 0 */
 /* SwiGLU then per-token int8 of the bf16 result (F % 8 == 0, F <= 32768) */

@@ -398,11 +398,15 @@ def test_w4a16_gemm(lib, oracle, M, N, K, group, sym, out):
     assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
 
 
-@pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (600, 4096, 14336)])
+@pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (600, 4096, 14336), (1849, 768, 4096)])
 def test_w4a16_gemm_llama_shapes_sampled_rows(lib, oracle, M, N, K):
-    """Full-size QKV (T=2192) and down-projection shapes: weights quantized on
+    """Full-size QKV (T=2192) and down-projection shapes, and the QKV
+    projection of one GPU's tensor-parallel shard (N = 6144 / 8: 45 tiles,
+    K in 4 spans; the down shape at M = 600 runs 2): weights quantized on
     the GPU (bit-exact quantizer), every output row of a sample checked
-    against the oracle, including the last, partial M tile."""
+    against the oracle, including the last, partial M tile; a second call
+    gives bit-identical output (the span sums' order does not depend on
+    which wave arrives last)."""
     print(f"[gpu] w4a16 gemm llama M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device=DEV).manual_seed(M)
     w = torch.randn((N, K), device=DEV, generator=g) * 0.02
@@ -422,6 +426,10 @@ def test_w4a16_gemm_llama_shapes_sampled_rows(lib, oracle, M, N, K):
                                  qz.cpu().numpy().view(np.uint32), None, N, K, 128)
     got = bf16_to_f32(u16(y)[rows])
     assert rel_err(got, yo) <= TOL_BF16
+    again = torch.empty_like(y)
+    lib.qlinear_w4a16(x, qw, sc, qz, None, G, again, 128)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int16), again.view(torch.int16))
 
 
 def test_w4a16_odd_group_uses_generic_path(lib, oracle):

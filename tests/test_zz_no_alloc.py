@@ -2,7 +2,10 @@
 SNEPPX_qlinear_w4a16 through the C-ABI: same kernels, so bit-identical
 outputs, on two calls in a row per path (the second smaller, reusing the
 static scratch array the first one filled), and a clear error for a call
-whose scratch would exceed the array."""
+whose scratch would exceed the array.  Where the allocating entry point
+splits the prefill GEMM's K into spans (few tiles), the allocation-free one
+runs it whole: the same product with another fp32 summation order, checked
+to the bf16 tolerance."""
 import numpy as np
 import pytest
 import torch
@@ -38,7 +41,7 @@ def _both(lib, M, N, K, seed, ydt=torch.bfloat16, bias=False):
 
 @pytest.mark.parametrize("first,second", [
     ((16, 11008, 14336), (8, 4096, 14336)),     # split-K partials: 9.9 MB, then 1.8 MB
-    ((1849, 4096, 4096), (300, 1000, 4096)),    # prefill GEMM, prepared activations: 15 MB, then 2.5 MB
+    ((1849, 4096, 4096), (300, 11008, 4096)),   # prefill GEMM, prepared activations: 15 MB, then 2.5 MB
     ((1, 11008, 4096), (4, 1000, 4096)),        # kernels without scratch
 ])
 def test_noalloc_matches_the_allocating_entry_point(lib, first, second):
@@ -46,6 +49,15 @@ def test_noalloc_matches_the_allocating_entry_point(lib, first, second):
         print(f"[gpu] noalloc M={M} N={N} K={K}", flush=True)
         y, y_ref = _both(lib, M, N, K, seed=M + N + i, bias=(i == 1))
         assert torch.equal(y.view(torch.int16), y_ref.view(torch.int16)), (M, N, K)
+
+
+def test_noalloc_where_the_allocating_entry_point_splits_k(lib):
+    # 12 tiles: the allocating entry point runs K in 4 spans, this one whole
+    for M, N, K in ((300, 1000, 4096), (1849, 768, 4096)):
+        print(f"[gpu] noalloc vs split M={M} N={N} K={K}", flush=True)
+        y, y_ref = _both(lib, M, N, K, seed=M + N)
+        a, b = y.float(), y_ref.float()
+        assert float((a - b).abs().max() / b.abs().max()) <= 1e-2, (M, N, K)
 
 
 def test_noalloc_fp32_output_and_bias(lib):
