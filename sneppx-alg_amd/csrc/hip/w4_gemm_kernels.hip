@@ -331,6 +331,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     }
     __builtin_amdgcn_s_waitcnt(0x0070);   // the ring's last (unused) loads drain before exit
 
+    bool last = true;                     // this wave writes its results (SPLIT: the last span to arrive)
     if constexpr (SPLIT > 1) {
         // slot (unit, wave): QM x FN results x 8 pieces of 16 B per lane, lane-major
         constexpr int NP = QM * FN * 8, SLOTB = NP * 64 * 16;
@@ -361,7 +362,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
         __builtin_amdgcn_sched_barrier(0);
         uint32_t c = 0;
         if (lane == 0) c = atomicAdd(&cnt[tile * 8 + wave], 1u);
-        if (__builtin_amdgcn_readfirstlane(c) != SPLIT - 1) return;
+        last = __builtin_amdgcn_readfirstlane(c) == SPLIT - 1;
+      if (last) {
         // the last wave of this (tile, wave): the spans' slots in span order, in
         // chunks of 4 pieces x SPLIT spans, each chunk's offsets carrying a zero
         // the previous chunk's sums produce (so the loads cannot all be hoisted)
@@ -401,6 +403,51 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                     asm volatile("s_mov_b32 %0, 0" : "=s"(dep) : "v"(p0 == 0 ? ch : cl));
                 }
         if (lane == 0) atomicExch(&cnt[tile * 8 + wave], 0u);   // ready for the next call
+      }
+    }
+
+    if constexpr (!SWIGLU) {
+        // 16-byte aligned output rows: each wave stages its RW x CW results in a
+        // private LDS region (after a barrier: every wave is past the ring and
+        // every direct load has landed) and writes them back as 16-byte row
+        // pieces, instead of one 2- or 4-byte store per value.  A wave reads
+        // back only what it wrote, so no barrier sits between the two.
+        constexpr int EB = YF32 ? 4 : 2, RB = CW * EB + 16, PPR = CW * EB / 16;
+        static_assert(8 * RW * RB <= GSTAGES * GRING, "the staged results fit in the ring");
+        if ((reinterpret_cast<uintptr_t>(y) & 15) == 0 && N % (16 / EB) == 0) {
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_barrier();
+            if (!last) return;
+            uint8_t* reg = lds + wave * (RW * RB);
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                const int n = n0 + wn * CW + j * 32 + r32;
+                const float bv = bias && n < N ? bias[n] : 0.0f;
+#pragma unroll
+                for (int i = 0; i < QM; i++)
+#pragma unroll
+                    for (int u = 0; u < 2; u++)
+#pragma unroll
+                        for (int v = 0; v < 16; v++) {
+                            const int row = 32 * (2 * i + u) + 8 * (v >> 2) + 4 * h + (v & 3);
+                            const float val = yq[i][j][16 * u + v] + bv;
+                            if (YF32)
+                                *reinterpret_cast<float*>(reg + row * RB + (j * 32 + r32) * 4) = val;
+                            else
+                                *reinterpret_cast<uint16_t*>(reg + row * RB + (j * 32 + r32) * 2) = bf16_out(val);
+                        }
+            }
+#pragma unroll
+            for (int t = 0; t < RW * PPR / 64; t++) {
+                const int q = t * 64 + lane, row = q / PPR, pc = q % PPR;
+                const int m = m0 + wm * RW + row, n = n0 + wn * CW + pc * (16 / EB);
+                const u32x4 val = *reinterpret_cast<const u32x4*>(reg + row * RB + pc * 16);
+                if (m < M && n < N)
+                    *reinterpret_cast<u32x4*>(reinterpret_cast<uint8_t*>(y) + ((size_t)m * N + n) * EB) = val;
+            }
+            return;
+        }
+        if (!last) return;
     }
 
     if constexpr (SWIGLU) {

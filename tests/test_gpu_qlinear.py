@@ -398,6 +398,31 @@ def test_w4a16_gemm(lib, oracle, M, N, K, group, sym, out):
     assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
 
 
+@pytest.mark.parametrize("N,out,yoff", [(1001, "f32", 0), (1004, "bf16", 0), (1000, "bf16", 2), (1000, "f32", 1),
+                                        (1000, "bf16", 0), (1000, "f32", 0)])
+def test_w4a16_gemm_output_rows_staged_or_not(lib, oracle, N, out, yoff):
+    """The prefill GEMM writes 16-byte row pieces staged through LDS when the
+    output rows allow it (16-byte aligned, N a multiple of 8 bf16 / 4 fp32
+    values) and one value per store otherwise: N = 1001 / 1004 and outputs
+    offset by 2 or 1 values take the second path; both against the oracle,
+    with a bias."""
+    M, K, group = 300, 1024, 128
+    print(f"[gpu] w4a16 gemm epilogue N={N} out={out} yoff={yoff}", flush=True)
+    qw, sc, qz, G = _w4_case(oracle, N, K, group, N + 3)
+    x = bf16_bits(np.random.default_rng(N).normal(0, 1, (M, K)).astype(np.float32))
+    b = np.random.default_rng(N + 1).normal(0, 1, N).astype(np.float32)
+    dt = torch.float32 if out == "f32" else torch.bfloat16
+    buf = torch.zeros(M * N + yoff, dtype=dt, device=DEV)
+    y = buf[yoff:].view(M, N)
+    lib.qlinear_w4a16(to_dev(x), to_dev(qw), to_dev(sc), to_dev(qz), None, G, y, group, bias=to_dev(b))
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, None, N, K, group, bias=b)
+    got = y.cpu().numpy() if out == "f32" else bf16_to_f32(u16(y))
+    assert rel_err(got, yo) <= (TOL_F32 if out == "f32" else TOL_BF16)
+    if yoff:
+        assert float(buf[:yoff].abs().max()) == 0.0       # nothing written before the output
+
+
 @pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (600, 4096, 14336), (1849, 768, 4096)])
 def test_w4a16_gemm_llama_shapes_sampled_rows(lib, oracle, M, N, K):
     """Full-size QKV (T=2192) and down-projection shapes, and the QKV
