@@ -752,16 +752,24 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
         }
     }
 
-    // 5. nibbles -> bf16 (128 + q), one and-or per pair; diagonal 4x4x4 MFMAs
+    // 5. nibbles -> bf16 (128 + q), one and-or per pair; diagonal 4x4x4 MFMAs.
+    // The weight loads are consumed in issue order (row 0's chunks, then row
+    // 1's), each chunk's products fenced from the next by a scheduling
+    // barrier, and row 0 is summed across the wave before row 1's loads are
+    // waited for: after the last load lands only one chunk's products, one
+    // wave sum and the stores remain.  The stores stay at the end: a store
+    // issued earlier counts in vmcnt and would make the waits for row 1's
+    // loads cover both of them.
     uint32_t nib_mask, bf_bias;
     asm volatile("s_mov_b32 %0, 0xf000f" : "=s"(nib_mask));
     asm volatile("v_mov_b32 %0, 0x43004300" : "=v"(bf_bias));
     typedef short s16x4 __attribute__((ext_vector_type(4)));
     typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-    f32x4 y4[RW];
+    const int dg = lane & 3;
+    float out[RW];
 #pragma unroll
     for (int r = 0; r < RW; r++) {
-        y4[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 y4 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < T; t++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -777,17 +785,13 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
                 acc = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a1),
                                                              __builtin_bit_cast(s16x4, b1), acc, 0, 0, 0);
             }
-            y4[r] += sc[r][t] * acc;
+            y4 += sc[r][t] * acc;
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
-
-    // 6. the lane's diagonal element, wave sum, one lane stores the rows
-    const int dg = lane & 3;
-    float out[RW];
-#pragma unroll
-    for (int r = 0; r < RW; r++) {
-        const float d = dg == 0 ? y4[r][0] : dg == 1 ? y4[r][1] : dg == 2 ? y4[r][2] : y4[r][3];
+        // 6. the lane's diagonal element, wave sum to lane 63
+        const float d = dg == 0 ? y4[0] : dg == 1 ? y4[1] : dg == 2 ? y4[2] : y4[3];
         out[r] = dpp_sum_to_lane63(d - corr[r]);
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (lane == 63 && GLU) {
         if (n0 < rend) {
