@@ -578,7 +578,6 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     uint32_t* ssc = reinterpret_cast<uint32_t*>(xsum + NCHM);            // [16 rows][GM/2 words]
     uint32_t* szr = ssc + WROWS * (GM / 2);                              // [16 rows][2T words]
     uint16_t* xraw = reinterpret_cast<uint16_t*>(szr + WROWS * ZPRM);    // PERM: [KM]
-    uint16_t* pl = xraw + KM;                                            // PERM: [KM]
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -675,17 +674,12 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
             const int it = tid + i * NTHR;
-            if (it < NIT) {
-                *reinterpret_cast<u32x4*>(xraw + it * 8) = xr[i];
-                *reinterpret_cast<u32x4*>(pl + it * 8) = pr[i];
-            }
+            if (it < NIT) *reinterpret_cast<u32x4*>(xraw + it * 8) = xr[i];
         }
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < XPT; i++) {
-            int it = tid + i * NTHR;
-            it = it < NIT ? it : NIT - 1;
-            const u32x4 pv = *reinterpret_cast<const u32x4*>(pl + it * 8);
+            const u32x4 pv = pr[i];   // the thread's own perm piece (of its clamped item)
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 uint32_t lo = pv[e] & 0xFFFFu, hi = pv[e] >> 16;
@@ -997,7 +991,7 @@ int launch_small_m(const W4Launch& a) {
 // next multiple of 2048).
 size_t gemv1_lds(size_t K, bool perm) {
     const size_t nch = K / 32, g = K / 128;
-    return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 4 * K : 0);
+    return nch * 80 + nch * 4 + 16 * (g / 2) * 4 + 16 * (g / 8) * 4 + (perm ? 2 * K : 0);
 }
 
 // Workgroups of the M = 1 kernel: enough for at most `per` rows each (16, or
@@ -1015,7 +1009,7 @@ template <int T, bool PERM, bool KR>
 int launch_gemv1_t(const W4Launch& a) {
     dim3 grid(gemv1_grid(a.N)), block(512);
     const size_t lds = gemv1_lds((size_t)(2048 * T), PERM);
-    if (lds > 64 * 1024) {   // PERM at K > 8192: the staged copies of x and perm
+    if (lds > 64 * 1024) {   // PERM at K > 12288: the staged copy of x
         static std::atomic<uint64_t> lds_done[4];   // (zeros, f32 out) variants, per device
         const void* kfn[4] = {reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, false, PERM, false, KR>),
                               reinterpret_cast<const void*>(&k_w4a16_gemv1<T, false, true, PERM, false, KR>),
