@@ -1107,7 +1107,7 @@ int launch_small(const W4Launch& a) {
 // workgroup (a CU returns its loads in issue order).  PERM: qw's columns are
 // stored in the order perm (uint16 [K]); the A fragments gather
 // x[m][perm[k']] from the LDS copy.
-template <int NC, bool ZEROS, bool YF32, bool PERM>
+template <int NC, bool ZEROS, bool YF32, bool PERM, int EARLY>
 __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restrict__ x,
                                                        const uint32_t* __restrict__ qw,
                                                        const uint16_t* __restrict__ scales,
@@ -1181,6 +1181,15 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
             if (it < KW) pr[i] = load16(perm + (size_t)it * 8);
         }
     }
+    // the first EARLY groups' weights go out right behind the activation (and
+    // perm) loads: the CU returns loads in issue order, so the copy below
+    // waits only for the activations while those weights stream.  More
+    // groups issued this early fill the CU's queue of outstanding loads and
+    // hold up the copy (EARLY = 2 pays from M = 12 on, where the copy itself
+    // is long; all three groups this early is slower at every M).
+    static_assert(EARLY == 1 || EARLY == 2, "one or two groups ahead of the copy");
+    wload(rg, wa, sa, za);
+    if constexpr (EARLY == 2) wload(rg + nb, wb, sb, zb);
 #pragma unroll
     for (int i = 0; i < XPT; i++) {
         const int it = tid + 512 * i;
@@ -1197,11 +1206,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
         }
     }
     lds_barrier();
-    // the first three groups' weights go out once the activations are in LDS:
-    // issued earlier, a wave blocks on its weight loads (the CU's queue of
-    // outstanding loads is full) before it can stage anything
-    wload(rg, wa, sa, za);
-    wload(rg + nb, wb, sb, zb);
+    // the remaining of the first three groups once the activations are in LDS
+    if constexpr (EARLY == 1) wload(rg + nb, wb, sb, zb);
     wload(rg + 2 * nb, wc, sc3, zc);
 
     // 2. the wave's A fragments: row l16 (zero beyond M), words
@@ -1310,19 +1316,31 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv_mt(const uint16_t* __restric
     }
 }
 
-template <int NC, bool Z, bool F, bool PERM>
-int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
-                   const uint16_t* perm, void* y, const float* bias, int M, int N, size_t lds, int grid,
-                   hipStream_t st) {
+template <int NC, bool Z, bool F, bool PERM, int EARLY>
+int launch_gemv_mt_e(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
+                     const uint16_t* perm, void* y, const float* bias, int M, int N, size_t lds, int grid,
+                     hipStream_t st) {
     // the LDS size depends on M: opt in to the most any call may ask for
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM>);
+    const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemv_mt<NC, Z, F, PERM, EARLY>);
     if (snx::lds_optin(kfn, 160 * 1024, lds_done) != hipSuccess) {
         snx_set_error("w4a16 gemv: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_w4a16_gemv_mt<NC, Z, F, PERM><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, bias, M, N);
+    k_w4a16_gemv_mt<NC, Z, F, PERM, EARLY><<<grid, 512, lds, st>>>(x, qw, scales, qz, perm, y, bias, M, N);
     return snx_launch_check("k_w4a16_gemv_mt");
+}
+
+// Measured at N = 11008, K = 4096: one group's weights ahead of the
+// activation copy is fastest up to M = 10 (8.1-8.5 against 8.5-8.8 us with
+// two), two from M = 12 (8.8-9.2 against 9.0-9.6 us).
+template <int NC, bool Z, bool F, bool PERM>
+int launch_gemv_mt(const uint16_t* x, const uint32_t* qw, const uint16_t* scales, const uint32_t* qz,
+                   const uint16_t* perm, void* y, const float* bias, int M, int N, size_t lds, int grid,
+                   hipStream_t st) {
+    if (M > 10)
+        return launch_gemv_mt_e<NC, Z, F, PERM, 2>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
+    return launch_gemv_mt_e<NC, Z, F, PERM, 1>(x, qw, scales, qz, perm, y, bias, M, N, lds, grid, st);
 }
 
 template <int NC, bool PERM>
