@@ -715,18 +715,24 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
     __syncthreads();
 
     // 4. this lane's activations, chunk sums, scales and zero-point correction
-    uint32_t xb[T][16];
+    // JIT (K > 8192): each chunk's activations are read from LDS where the
+    // chunk is used (once per row) instead of being held for both rows: 16
+    // registers instead of 16 T, so two workgroups fit on a CU.
+    constexpr bool JIT = T >= 5;
+    uint32_t xb[JIT ? 1 : T][16];
     float X[T];
 #pragma unroll
     for (int t = 0; t < T; t++) {
         const int c = 64 * t + lane;
+        if (!JIT) {
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(smem + c * 80 + q * 16);
-            xb[t][4 * q] = v[0];
-            xb[t][4 * q + 1] = v[1];
-            xb[t][4 * q + 2] = v[2];
-            xb[t][4 * q + 3] = v[3];
+            for (int q = 0; q < 4; q++) {
+                const u32x4 v = *reinterpret_cast<const u32x4*>(smem + c * 80 + q * 16);
+                xb[JIT ? 0 : t][4 * q] = v[0];
+                xb[JIT ? 0 : t][4 * q + 1] = v[1];
+                xb[JIT ? 0 : t][4 * q + 2] = v[2];
+                xb[JIT ? 0 : t][4 * q + 3] = v[3];
+            }
         }
         X[t] = xsum[c];
     }
@@ -767,13 +773,27 @@ __global__ void __launch_bounds__(512) k_w4a16_gemv1(const uint16_t* __restrict_
 #pragma unroll
         for (int t = 0; t < T; t++) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            uint32_t xc[16];
+            if constexpr (JIT) {
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const u32x4 v = *reinterpret_cast<const u32x4*>(smem + (64 * t + lane) * 80 + q * 16);
+                    xc[4 * q] = v[0];
+                    xc[4 * q + 1] = v[1];
+                    xc[4 * q + 2] = v[2];
+                    xc[4 * q + 3] = v[3];
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; q++) xc[q] = xb[JIT ? 0 : t][q];
+            }
 #pragma unroll
             for (int d = 0; d < 4; d++) {
                 const uint32_t w = wv[r][t][d];
                 const u32x2 a0 = {(w & nib_mask) | bf_bias, ((w >> 4) & nib_mask) | bf_bias};
                 const u32x2 a1 = {((w >> 8) & nib_mask) | bf_bias, ((w >> 12) & nib_mask) | bf_bias};
-                const u32x2 b0 = {xb[t][4 * d], xb[t][4 * d + 1]};
-                const u32x2 b1 = {xb[t][4 * d + 2], xb[t][4 * d + 3]};
+                const u32x2 b0 = {xc[4 * d], xc[4 * d + 1]};
+                const u32x2 b1 = {xc[4 * d + 2], xc[4 * d + 3]};
                 acc = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a0),
                                                              __builtin_bit_cast(s16x4, b0), acc, 0, 0, 0);
                 acc = __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4, a1),
