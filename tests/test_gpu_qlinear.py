@@ -255,6 +255,29 @@ def test_w4a16_actorder_prepared_ragged_k(lib, oracle, K, zeros):
     assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
 
 
+@pytest.mark.parametrize("M,zeros", [(11, False), (16, True), (12, True)])
+def test_w4a16_actorder_prepared_small_m_two_early_groups(lib, oracle, M, zeros):
+    """Act-order weights at 11 <= M <= 16 through the small-M kernel's form
+    that issues two row groups' weight loads ahead of the activation copy
+    (N = 11008: three groups per workgroup), against the oracle on the
+    original column order."""
+    N, K = 11008, 4096
+    print(f"[gpu] w4a16 act-order prepared M={M} zeros={zeros}", flush=True)
+    rng = np.random.default_rng(100 + M)
+    g_idx = (rng.permutation(K) // 128).astype(np.int32)
+    qw, sc, _, G = _w4_case(oracle, N, K, 128, 31, g_idx=g_idx)
+    qz = rng.integers(0, 2**32, (N, (G + 7) // 8), dtype=np.uint64).astype(np.uint32) if zeros else None
+    x = bf16_bits(rng.normal(0, 1, (M, K)).astype(np.float32))
+    qs = torch.empty((N, K // 8), dtype=torch.int32, device=DEV)
+    perm = torch.empty(K, dtype=torch.int16, device=DEV)
+    lib.qlinear_w4_actorder_prepare(to_dev(qw), to_dev(g_idx), G, qs, perm)
+    y = torch.empty((M, N), dtype=torch.float32, device=DEV)
+    lib.qlinear_w4a16_actorder(to_dev(x), qs, to_dev(sc), None if qz is None else to_dev(qz), perm, y, 128)
+    torch.cuda.synchronize()
+    rc, yo = oracle.w4a16_linear(x, qw, sc, qz, g_idx, N, K, 128)
+    assert rel_err(y.cpu().numpy(), yo) <= TOL_F32
+
+
 @pytest.mark.parametrize("M,N,K,sym,out", [
     (2, 8197, 1024, False, "f32"), (3, 45, 2048, True, "bf16"), (5, 4099, 3072, False, "f32"),
     (8, 11008, 4096, True, "f32"), (16, 300, 4096, False, "bf16"), (16, 9000, 2048, True, "f32"),
