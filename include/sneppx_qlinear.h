@@ -86,8 +86,10 @@ int SNEPPX_dev_quantize_w4_gptq(const float* w, const int32_t* g_idx, size_t G,
                                 size_t N, size_t K, SNEPPXStream stream);
 
 /* Per-tensor scaled FP8 E4M3 with the reference encoder (quantize_fp8.c:41-69):
- * s = max|x|/240 (1 when below FLT_MIN), code = e4m3(x * (1/s)).  *scale_out
- * is a device float. */
+ * s = max|x|/240 (1 when below FLT_MIN), code = e4m3(x / s), a correctly
+ * rounded division (not x * (1/s): the two differ in the last bit, which the
+ * truncating encoder can turn into a whole code step).  *scale_out is a
+ * device float. */
 int SNEPPX_dev_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, float* scale_out,
                                         size_t n, SNEPPXStream stream);
 

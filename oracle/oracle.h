@@ -146,7 +146,10 @@ void orc_i8_gemm_i32(const int8_t* A, const int8_t* W, int32_t* C,
 /* out[m][n] = ((float)acc * sA[m]) * sW[n] (fp32) */
 void orc_w8a8_epilogue(const int32_t* acc, const float* sA, const float* sW,
                        size_t M, size_t N, float* out);
-/* per-tensor fp8: s = amax/240 (1 if amax < FLT_MIN), code = e4m3(x * (1/s)) */
+/* per-tensor fp8 (build-defined): s = amax/240 (1 if
+ * amax < FLT_MIN), code = e4m3(x / s) with the reference encoder of
+ * quantize_fp8.c:41-69.  Pinned by planted tensors whose x / s and
+ * x * (1/s) give different codes. */
 int orc_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, size_t n, float* scale_out);
 /* out[m][n] = (sum_k dec(A)*dec(W), k ascending) * sA * sW */
 void orc_fp8_gemm(const uint8_t* A, const uint8_t* W, float sA, float sW,

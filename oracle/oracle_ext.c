@@ -311,9 +311,8 @@ int orc_quantize_fp8_e4m3_scaled(const float* in, uint8_t* out, size_t n, float*
         if (a > m) m = a;
     }
     float s = m < FLT_MIN ? 1.0f : m / 240.0f;
-    float inv = 1.0f / s;
     *scale_out = s;
-    for (size_t i = 0; i < n; i++) out[i] = orc_float_to_fp8_e4m3(in[i] * inv);
+    for (size_t i = 0; i < n; i++) out[i] = orc_float_to_fp8_e4m3(in[i] / s);
     return 0;
 }
 

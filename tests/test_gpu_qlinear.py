@@ -123,6 +123,28 @@ def test_dev_fp8_scaled_bit_exact(lib, oracle, n):
     assert np.array_equal(out.cpu().numpy(), co) and s.item() == so
 
 
+def test_dev_fp8_scaled_division_rule(lib, oracle):
+    """Tensors whose largest element is coded 0x77 under x / s and 0x76
+    under x * (1/s), and the other way round: the kernel must give the
+    oracle's (division) codes for both."""
+    rng = np.random.default_rng(23)
+    am = rng.uniform(0.5, 8.0, 4000).astype(np.float32)
+    sc = (am / np.float32(240)).astype(np.float32)
+    vd = (am / sc).astype(np.float32)
+    vm = (am * (np.float32(1) / sc).astype(np.float32)).astype(np.float32)
+    picks = np.concatenate([am[(vd >= 240) & (vm < 240)][:8], am[(vd < 240) & (vm >= 240)][:8]])
+    assert len(picks) == 16
+    for i, a in enumerate(picks):
+        x = np.clip(rng.normal(0, float(a) / 4, 4099), -a, a).astype(np.float32)
+        x[(37 * i) % 4099] = a if i % 2 else -a
+        out = torch.empty(x.size, dtype=torch.uint8, device=DEV)
+        s = torch.empty(1, device=DEV)
+        lib.dev_quantize_fp8_e4m3_scaled(to_dev(x), out, s)
+        torch.cuda.synchronize()
+        rc, co, so = oracle.quantize_fp8_e4m3_scaled(x)
+        assert np.array_equal(out.cpu().numpy(), co) and s.item() == so, a
+
+
 # ---------------------------------------------------------------- linears
 @pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (4, 1000, 4096), (2, 37, 100), (1, 17, 1024),
                                    (1, 1001, 2048), (1, 300, 8192), (1, 1, 4096), (1, 4096, 14336),

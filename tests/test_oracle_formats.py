@@ -276,3 +276,103 @@ def test_bias_step(oracle):
     assert np.abs(y - want).max() <= 1e-5 * np.abs(want).max()
     rc, ynb = oracle.w4a16_linear(xb, qw, sc, qz, None, N, K, g)
     assert np.array_equal(y, (ynb + bias[None, :]).astype(np.float32))
+
+
+def _planted_fp8_amax(rng, want_div_at_240):
+    """amax values whose per-tensor fp8 codes differ between x / s and
+    x * (1/s) with s = amax / 240: with want_div_at_240 the quotient is 240
+    (code 0x77) and the product 239.99998 (0x76), else the other way."""
+    am = rng.uniform(0.5, 8.0, 4000).astype(np.float32)
+    s = (am / np.float32(240)).astype(np.float32)
+    inv = (np.float32(1) / s).astype(np.float32)
+    vd = (am / s).astype(np.float32)
+    vm = (am * inv).astype(np.float32)
+    sel = (vd >= 240) & (vm < 240) if want_div_at_240 else (vd < 240) & (vm >= 240)
+    return am[sel]
+
+
+def test_fp8_per_tensor_rule_is_division(oracle):
+    """The per-tensor fp8 quantizer encodes x / s (one correctly rounded
+    division), not x * (1/s).  Each planted tensor's largest element lands
+    at 240 under one rule and 239.99998 under the other, which the
+    reference's truncating encoder sends to 0x77 and 0x76; the oracle must
+    give the division's code for every element, in both directions.  The
+    expected codes use the reference array encoder (quantize_fp8.c:111-121,
+    pinned exhaustively against the reference build) on numpy's fp32
+    quotient."""
+    rng = np.random.default_rng(21)
+    for want_div_at_240 in (True, False):
+        amaxes = _planted_fp8_amax(rng, want_div_at_240)[:24]
+        assert len(amaxes) >= 8
+        for i, am in enumerate(amaxes):
+            x = rng.normal(0, float(am) / 4, 257).astype(np.float32)
+            x = np.clip(x, -am, am)
+            x[i % 257] = am if i % 2 == 0 else -am
+            rc, c, s = oracle.quantize_fp8_e4m3_scaled(x)
+            assert rc == 0 and s == (np.float32(am) / np.float32(240)).astype(np.float32)
+            _, want = oracle.quantize_fp8((x / s).astype(np.float32))
+            _, mul = oracle.quantize_fp8((x * (np.float32(1) / s)).astype(np.float32))
+            assert np.array_equal(c, want), (am, np.flatnonzero(c != want))
+            top = c[i % 257] & 0x7F
+            assert top == (0x77 if want_div_at_240 else 0x76)
+            assert (mul[i % 257] & 0x7F) == (0x76 if want_div_at_240 else 0x77)
+            assert not np.array_equal(c, mul)
+    # degenerate tensor: scale 1, raw codes
+    rc, c, s = oracle.quantize_fp8_e4m3_scaled(np.zeros(5, np.float32))
+    assert rc == 0 and s == 1.0 and not c.any()
+
+
+def test_actorder_dequant_gathers_by_g_idx(oracle, golden):
+    """orc_w4_dequantize with g_idx reads scale[n][g_idx[k]] for column k.
+    Closed form against the reference's own GPTQ output: after the stable
+    argsort perm of g_idx, column perm[i] holds the reference code
+    q_perm[n][i] of group i // 128, so its dequantised value is exactly
+    q_perm * fp16(s) (a product of a 4-bit integer and an fp16 value is
+    exact in fp32).  A k // 128 gather (the no-g_idx path) fails it."""
+    f = cases(golden, "actorder")["actorder"]
+    w, g_idx, perm, q_perm, s = f["w"], f["g_idx"], f["perm"], f["q_perm"], f["s"]
+    N, K = w.shape
+    G = int(g_idx.max()) + 1
+    gs = K // G
+    rc, qw, sc = oracle.w4_gptq_quantize(w, g_idx, G)
+    assert rc == 0
+    rc, deq = oracle.w4_dequantize(qw, sc, None, g_idx, N, K, gs)
+    assert rc == 0
+    s16 = s.astype(np.float16).astype(np.float32)
+    want = np.zeros((N, K), np.float32)
+    grp_sorted = np.arange(K) // gs
+    want[:, perm] = q_perm.astype(np.float32) * s16[:, grp_sorted]
+    assert np.array_equal(deq, want)
+    # the planted mistake: gather by k // group instead of g_idx[k]
+    rc, wrong = oracle.w4_dequantize(qw, sc, None, None, N, K, gs)
+    assert rc == 0 and not np.array_equal(wrong, want)
+
+
+def test_actorder_dequant_error_bound_with_spread_groups(oracle):
+    """Invariant: after the act-order quantize, every element satisfies
+    |deq - w| <= s/2 + 7 |fp16(s) - s| with its own group's fp32 scale
+    s = max|w_group| / 7 (codes come from the fp32 scale, dequantisation
+    uses the stored fp16 one).  Groups get magnitudes 2^j apart, so reading
+    a neighbour's scale (a k // 128 gather) breaks the bound."""
+    rng = np.random.default_rng(22)
+    N, K, gs = 6, 1024, 128
+    G = K // gs
+    perm = rng.permutation(K)
+    g_idx = (perm // gs).astype(np.int32)               # each group: 128 scattered columns
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    w *= (2.0 ** g_idx.astype(np.float32))[None, :]
+    rc, qw, sc = oracle.w4_gptq_quantize(w, g_idx, G)
+    assert rc == 0
+    gmax = np.zeros((N, G), np.float32)
+    for j in range(G):
+        gmax[:, j] = np.abs(w[:, g_idx == j]).max(1)
+    s32 = (gmax / np.float32(7)).astype(np.float32)
+    s16 = sc.view(np.float16).astype(np.float64)
+    bound = 0.5 * s32.astype(np.float64) + 7 * np.abs(s16 - s32) + 1e-12
+    rc, deq = oracle.w4_dequantize(qw, sc, None, g_idx, N, K, gs)
+    assert rc == 0
+    err = np.abs(deq.astype(np.float64) - w.astype(np.float64))
+    assert np.all(err <= bound[:, g_idx] * (1 + 1e-6))
+    rc, wrong = oracle.w4_dequantize(qw, sc, None, None, N, K, gs)
+    err_w = np.abs(wrong.astype(np.float64) - w.astype(np.float64))
+    assert (err_w > bound[:, g_idx] * (1 + 1e-6)).mean() > 0.5
