@@ -76,14 +76,18 @@ class Timer:
         """Back-to-back time of `steps` calls between two events; `loop(n)`,
         when given, issues n calls from C (bench_loop.c) instead of Python."""
         import torch
+        a, b = self.lib.event(), self.lib.event()
+        torch.cuda.synchronize()
         if loop:
             loop(warmup)
         else:
             for i in range(warmup):
                 calls[i % len(calls)]()
-        torch.cuda.synchronize()
-        # whole-job time: back-to-back launches between two events
-        a, b = self.lib.event(), self.lib.event()
+        # whole-job time: back-to-back launches between two events.  The
+        # start event is queued right behind the warm-up launches (no host
+        # synchronisation in between), so the timed launches begin on a busy
+        # queue: the first launch's wake-up latency stays in the warm-up and
+        # a short run times the same steady state as a long one.
         self.lib.record(a, self.stream)
         if loop:
             loop(steps)
@@ -91,8 +95,8 @@ class Timer:
             for i in range(steps):
                 calls[i % len(calls)]()
         self.lib.record(b, self.stream)
-        total_ms = self.lib.elapsed_ms(a, b)
         torch.cuda.synchronize()
+        total_ms = self.lib.elapsed_ms(a, b)
         # per-launch duration: an event pair around every launch
         evs = [(self.lib.event(), self.lib.event()) for _ in range(steps)]
         for i in range(steps):
@@ -888,7 +892,7 @@ def main():
     print(f"[bench] C2 M=1: {head['gbs']:.0f} GB/s whole-job, kernel {head['launch_ms_mean'] * 1e3:.2f} us",
           file=sys.stderr, flush=True)
 
-    extra, cpu_jobs = [], []
+    extra, cpu_jobs, gemm = [], [], {}
     if not args.no_extra:
         for m in (4, 16):
             r, (ws_m, x_m, _, _) = bench_w4a16(lib, timer, torch, m, N, K, group, args.copies,
@@ -940,11 +944,16 @@ def main():
         for fp8 in (False, True):
             r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP, fp8=fp8)
             peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS
+            kind = "fp8" if fp8 else "int8"
             extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N=14336 K=4096",
                           "value": round(r["tops"], 1), "unit": "TOPS",
                           "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4),
-                          "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
+                          "kernel_tops": round(r["tops_kernel"], 1), "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
+            gemm[kind] = dict(r, peak=peak, line=extra[-1])
             cpu_jobs.append((extra[-1], "fp8" if fp8 else "i8", r["host"]))
+            print(f"[bench] C4 W8A8 {kind} GEMM M=2048 N=14336 K=4096: {r['tops']:.0f} TOPS "
+                  f"({r['tops'] / peak:.4f} of {peak:.0f}), {r['ms_per_step'] * 1e3:.1f} us/launch",
+                  file=sys.stderr, flush=True)
         torch.cuda.synchronize()
         extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP))
         for fmt, peak in MX_BENCH.items():
@@ -981,6 +990,10 @@ def main():
         from py_oracle import Oracle
         cpu_legs(Oracle(perf=True), cpu_jobs, min(3.0, args.cpu_seconds))
         print(f"[bench] CPU legs done ({len(cpu_jobs)} configs)", file=sys.stderr, flush=True)
+        for kind, g in gemm.items():
+            cb = g["line"].get("cpu_baseline") or {}
+            print(f"[bench] CPU baseline C4 {kind}: {cb.get('value')} {cb.get('unit')} ({cb.get('sample')})",
+                  file=sys.stderr, flush=True)
 
     # per-launch duration = back-to-back time / launches (>= kernel time; it
     # matches rocprofv3's kernel-trace average to within the launch gap)
@@ -1011,9 +1024,38 @@ def main():
                      "event_pair_us_median": round(head["launch_ms_median"] * 1e3, 3),
                      "event_pair_us_p10_p90": [round(head_pcts[0] * 1e3, 3), round(head_pcts[1] * 1e3, 3)]},
         "cpu_baseline": cpu,
+        "roofline_gemm": roofline_gemm(gemm),
         "extra": extra,
     }
+    # the metric's second half (C4 W8A8 at M=2048) as flat scalars of the
+    # headline roofline too, next to the GEMV figures
+    for kind, g in gemm.items():
+        line["roofline"][f"c4_{kind}_tops"] = round(g["tops"], 1)
+        line["roofline"][f"c4_{kind}_frac"] = round(g["tops"] / g["peak"], 4)
+        line["roofline"][f"c4_{kind}_us"] = round(g["ms_per_step"] * 1e3, 2)
+        cb = g["line"].get("cpu_baseline") or {}
+        if cb.get("value") is not None:
+            line["cpu_baseline"] = dict(line["cpu_baseline"] or {})
+            line["cpu_baseline"][f"c4_{kind}_{cb.get('unit', 'TOPS')}"] = cb["value"]
     print(json.dumps(line), flush=True)
+
+
+def roofline_gemm(gemm):
+    """Roofline of the W8A8 GEMM (k_gemm_8wp) at C4: algorithmic ops per
+    launch over the back-to-back launch time, against dense int8 / fp8 MFMA
+    peak, with the HBM traffic the counters measured for one launch and the
+    same-run CPU baseline."""
+    if not gemm:
+        return None
+    out = {"bound": "mfma", "kernel": "k_gemm_8wp", "unit": "TOPS", "workload": "C4 M=2048 N=14336 K=4096",
+           "ops_per_launch": 2 * 2048 * 14336 * 4096}
+    for kind, g in gemm.items():
+        out[kind] = {"achieved": round(g["tops"], 1), "peak": g["peak"], "frac": round(g["tops"] / g["peak"], 4),
+                     "kernel_event_pair_tops": round(g["tops_kernel"], 1),
+                     "launch_us": round(g["ms_per_step"] * 1e3, 2),
+                     "traffic": load_traffic(f"k_gemm_8wp<{kind}>"),
+                     "cpu_baseline": g["line"].get("cpu_baseline")}
+    return out
 
 
 if __name__ == "__main__":

@@ -44,6 +44,15 @@ typedef void* SNEPPXStream;
 /* No reference counterpart: last error of this thread, "" if none. */
 const char* SNEPPX_qlinear_last_error(void);
 
+/* No reference counterpart, for callers that destroy streams: frees
+ * (ordered after the work already queued on `stream`) the scratch
+ * workspaces the calling thread holds for `stream` and those that ended
+ * threads left on it.  Call it before hipStreamDestroy.  Workspaces are
+ * otherwise kept per (device, stream, slot) for each host thread and pass to
+ * a later thread when their thread ends, so they do not grow with the number
+ * of threads that ever called.  Returns 0. */
+int SNEPPX_qlinear_release_workspaces(SNEPPXStream stream);
+
 /* ---- device quantizers (bit-exact with the host API / reference) ------- */
 
 /* Device form of SNEPPX_quantize_int8_channel (quantize_int8.c:157-177):
@@ -114,7 +123,11 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
  * reference).  For callers that cannot allocate device memory: code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc.
  * Same arguments, dispatch and results (bit-identical) as
- * SNEPPX_qlinear_w4a16, but the scratch the split-K decode and the prefill
+ * SNEPPX_qlinear_w4a16, with one exception: where the allocating entry point
+ * splits the prefill GEMM's K into spans (few output tiles, e.g. one GPU's
+ * tensor-parallel QKV shard), this one runs that GEMM whole-K, the same
+ * product with another fp32 summation order, so a bf16 output can differ
+ * in its last bit.  The scratch the split-K decode and the prefill
  * GEMM need (fp32 partials, prepared activations) comes from one static
  * device array of SNEPPX_NOALLOC_SCRATCH_BYTES per GPU, held from the first
  * call on that GPU until the process ends, instead of a workspace.  A call

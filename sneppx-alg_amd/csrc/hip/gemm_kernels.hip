@@ -842,8 +842,8 @@ constexpr uint32_t BUF_DROP = 0x7ffffff0u;   // store offset outside every outpu
 // with the same policy, so no copy an L2 holds is used, and no fence has to
 // write back or drop whole caches.  No wave waits for another, so
 // the result does not depend on which units are resident together.
-constexpr int PCROW = 120;
-constexpr int kSysCoherent = 1 | 16;   // buffer cache policy sc0 sc1: system-coherent access   // u16 per staged output row of a wave: 112 + 8 pad
+constexpr int PCROW = 120;             // u16 per staged output row of a wave: 112 + 8 pad
+constexpr int kSysCoherent = 1 | 16;   // buffer cache policy sc0 sc1: system-coherent access
 static_assert(8 * 32 * PCROW * 2 <= TLDS_STAGE, "a pass of every wave fits in one stage buffer");
 // A tile's int8 row / column scales and its bias wait in LDS beside the ring
 // (256 floats each, loaded straight from global memory when the tile starts)

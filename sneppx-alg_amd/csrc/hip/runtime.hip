@@ -5,14 +5,15 @@
 #include <atomic>
 #include <cstdint>
 #include <mutex>
-#include <vector>
 
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
 
 #include "snx_hip.h"
+#include "sneppx_qlinear.h"
 #include "../snx_internal.h"
+#include "../ws_registry.h"
 
 namespace {
 thread_local char g_err[512];
@@ -29,6 +30,39 @@ hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 // caller capturing the stream into a graph records an ordinary kernel node)
 __global__ void __launch_bounds__(256) k_fill_zero_u32(uint32_t* __restrict__ p, size_t n) {
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+}  // namespace
+
+// The library's internal scratch (split-K partials, prepared activations,
+// gathers) comes from per-thread workspaces keyed by (device, stream, slot):
+// ws_registry.h holds the rules (no sharing between threads, stream-ordered
+// growth, buffers of ended threads adopted by later ones).  Here it gets the
+// device side: the stream-ordered pool, and a fill kernel for zeroed
+// buffers.
+namespace {
+void* ws_alloc(size_t bytes, void* stream, bool zeroed) {
+    void* p = nullptr;
+    if (snx_hip_malloc_async(&p, bytes, stream)) return nullptr;
+    if (zeroed) {
+        const size_t n = bytes / 4;
+        k_fill_zero_u32<<<(unsigned)(n / 256 < 1024 ? (n + 255) / 256 : 1024), 256, 0, S(stream)>>>(
+            static_cast<uint32_t*>(p), n);
+        if (snx_launch_check("k_fill_zero_u32")) {
+            (void)hipFreeAsync(p, S(stream));
+            return nullptr;
+        }
+    }
+    return p;
+}
+
+void ws_release(void* p, void* stream) { (void)hipFreeAsync(p, S(stream)); }
+
+void* workspace(size_t bytes, int slot, void* stream, bool zeroed) {
+    static std::once_flag once;
+    std::call_once(once, [] { snx_ws::init(ws_alloc, ws_release); });
+    int dev = 0;
+    if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
+    return snx_ws::get(dev, stream, slot, bytes, zeroed);
 }
 }  // namespace
 
@@ -95,65 +129,6 @@ int snx_hip_free_async(void* ptr, void* stream) {
     return ptr ? check(hipFreeAsync(ptr, S(stream)), "hipFreeAsync") : 0;
 }
 
-// Workspaces kept per (device, stream, slot, host thread) for the library's
-// internal scratch (split-K partials, prepared activations, gathers).  Work
-// on one stream runs in order, so a call may reuse its buffer without
-// waiting; a larger request releases the old buffer stream-ordered (after
-// the work already queued on that stream) and takes a new one from the pool.
-// Keying by thread as well means two host threads never share a buffer, even
-// when they enqueue on the same stream: one thread's stream-ordered release
-// can only follow that thread's own earlier work.  A thread's buffers live
-// until snx_release_workspaces(stream) or the end of the process.
-namespace {
-struct Workspace {
-    int dev, slot, thread;
-    void* stream;
-    void* ptr;
-    size_t bytes;
-};
-std::mutex g_ws_mu;
-std::vector<Workspace> g_ws;
-std::atomic<int> g_thread_ids{0};
-
-int thread_key() {
-    thread_local int id = g_thread_ids.fetch_add(1, std::memory_order_relaxed);
-    return id;
-}
-}  // namespace
-
-namespace {
-void* workspace(size_t bytes, int slot, void* stream, bool zeroed) {
-    int dev = 0;
-    if (check(hipGetDevice(&dev), "hipGetDevice")) return nullptr;
-    if (bytes == 0) bytes = 1;
-    const int th = thread_key();
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    Workspace* w = nullptr;
-    for (auto& e : g_ws)
-        if (e.dev == dev && e.slot == slot && e.stream == stream && e.thread == th) w = &e;
-    if (w && w->bytes >= bytes) return w->ptr;
-    const size_t want = (bytes + (bytes >> 2) + 4095) & ~(size_t)4095;   // +25% headroom
-    void* p = nullptr;
-    if (snx_hip_malloc_async(&p, want, stream)) return nullptr;
-    if (zeroed) {
-        k_fill_zero_u32<<<(unsigned)(want / 4 / 256 < 1024 ? (want / 4 + 255) / 256 : 1024), 256, 0, S(stream)>>>(
-            static_cast<uint32_t*>(p), want / 4);
-        if (snx_launch_check("k_fill_zero_u32")) {
-            (void)snx_hip_free_async(p, stream);
-            return nullptr;
-        }
-    }
-    if (w) {
-        if (snx_hip_free_async(w->ptr, stream)) return nullptr;
-        w->ptr = p;
-        w->bytes = want;
-    } else {
-        g_ws.push_back(Workspace{dev, slot, th, stream, p, want});
-    }
-    return p;
-}
-}  // namespace
-
 void* snx_workspace(size_t bytes, int slot, void* stream) { return workspace(bytes, slot, stream, false); }
 
 // As snx_workspace, with a new buffer zero-filled (stream-ordered) when it is
@@ -161,21 +136,17 @@ void* snx_workspace(size_t bytes, int slot, void* stream) { return workspace(byt
 // split GEMM's arrival counters).
 void* snx_workspace_zeroed(size_t bytes, int slot, void* stream) { return workspace(bytes, slot, stream, true); }
 
-// Frees (stream-ordered) every workspace of this thread on `stream`, for a
-// caller about to destroy that stream.
-void snx_release_workspaces(void* stream) {
-    const int th = thread_key();
-    std::lock_guard<std::mutex> lock(g_ws_mu);
-    for (size_t i = 0; i < g_ws.size();) {
-        if (g_ws[i].stream == stream && g_ws[i].thread == th) {
-            (void)hipFreeAsync(g_ws[i].ptr, S(stream));
-            g_ws[i] = g_ws.back();
-            g_ws.pop_back();
-        } else {
-            i++;
-        }
-    }
+// Frees (stream-ordered) this thread's workspaces on `stream` and those that
+// ended threads left on it, for a caller about to destroy that stream.
+void snx_release_workspaces(void* stream) { snx_ws::release_stream(stream); }
+
+int SNEPPX_qlinear_release_workspaces(SNEPPXStream stream) {
+    snx_ws::release_stream(stream);
+    return 0;
 }
+
+// Workspaces currently held (by live threads and left by ended ones).
+long snx_workspace_count(void) { return snx_ws::live(); }
 
 int snx_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
     if (bytes == 0) return 0;

@@ -21,8 +21,11 @@ void snx_set_error(const char* fmt, ...);
 void* snx_workspace(size_t bytes, int slot, void* stream);
 /* as snx_workspace; a newly taken buffer is zero-filled on `stream` first */
 void* snx_workspace_zeroed(size_t bytes, int slot, void* stream);
-/* stream-ordered release of the calling thread's workspaces on `stream` */
+/* stream-ordered release of the calling thread's workspaces on `stream` and
+ * of those that ended threads left on it */
 void snx_release_workspaces(void* stream);
+/* workspaces held now, by live threads and left by ended ones (for tests) */
+long snx_workspace_count(void);
 /* the current device's static scratch array (noalloc.hip) when `bytes` fit
  * in it, else NULL with the error text set (prefixed by `who`) */
 void* snx_noalloc_scratch(size_t bytes, const char* who);

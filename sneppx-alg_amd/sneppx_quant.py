@@ -146,6 +146,8 @@ EXPORTS = {
     "snx_hip_event_elapsed_ms": (C.c_int, [C.POINTER(C.c_float), _vp, _vp]),
     "snx_hip_stream_sync": (C.c_int, [_vp]),
     "snx_hip_device_info": (C.c_int, [C.c_char_p, _sz, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
+    "SNEPPX_qlinear_release_workspaces": (C.c_int, [_vp]),
+    "snx_workspace_count": (C.c_long, []),
 }
 
 
@@ -163,6 +165,26 @@ def _ptr(t):
     if t is None:
         return None
     return C.c_void_p(t.data_ptr())
+
+
+def _bias_ptr(bias, n, like):
+    """Pointer of an optional bias after checking what the kernels read: fp32,
+    contiguous, on the output's device, exactly n elements (2F for the stacked
+    gate/up of the SwiGLU form).  Anything else raises ValueError rather than
+    letting a kernel read past the end or reinterpret bf16 bits."""
+    if bias is None:
+        return None
+    if not isinstance(bias, torch.Tensor):
+        raise ValueError("bias must be a torch tensor on the device (fp32 [N])")
+    if bias.dtype != torch.float32:
+        raise ValueError(f"bias must be float32, got {bias.dtype}")
+    if not bias.is_contiguous():
+        raise ValueError("bias must be contiguous")
+    if bias.device != like.device:
+        raise ValueError(f"bias is on {bias.device}, the output on {like.device}")
+    if bias.numel() != n:
+        raise ValueError(f"bias has {bias.numel()} elements, the linear needs {n}")
+    return C.c_void_p(bias.data_ptr())
 
 
 class Library:
@@ -336,7 +358,7 @@ class Library:
         M, K = x.shape
         N = qweight.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8_gemv"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(bias), _ptr(y), M, N, K, self._stream(stream)),
+            _ptr(x), _ptr(qweight), _ptr(scales), _bias_ptr(bias, N, y), _ptr(y), M, N, K, self._stream(stream)),
             "qlinear_w8_gemv")
 
     def qlinear_w4a16(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None, bias=None):
@@ -344,7 +366,7 @@ class Library:
         N = qweight.shape[0]
         ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
         self.check(self.fn["SNEPPX_qlinear_w4a16"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(bias), _ptr(y),
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _bias_ptr(bias, N, y), _ptr(y),
             ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16")
 
     def qlinear_w4a16_noalloc(self, x, qweight, scales, qzeros, g_idx, G, y, group, stream=None,
@@ -355,7 +377,7 @@ class Library:
         N = qweight.shape[0]
         ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
         self.check(self.fn["SNEPPX_qlinear_w4a16_noalloc"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _ptr(bias), _ptr(y),
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(g_idx), G, _bias_ptr(bias, N, y), _ptr(y),
             ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16_noalloc")
 
     def qlinear_w4_actorder_prepare(self, qweight, g_idx, G, qweight_sorted, perm, stream=None):
@@ -370,7 +392,7 @@ class Library:
         N = qweight_sorted.shape[0]
         ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
         self.check(self.fn["SNEPPX_qlinear_w4a16_actorder"](
-            _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _ptr(bias), _ptr(y),
+            _ptr(x), _ptr(qweight_sorted), _ptr(scales), _ptr(qzeros), _ptr(perm), _bias_ptr(bias, N, y), _ptr(y),
             ydt, M, N, K, group, self._stream(stream)), "qlinear_w4a16_actorder")
 
     def qlinear_w4a16_swiglu(self, x, qweight, scales, qzeros, out, group, stream=None, bias=None):
@@ -378,7 +400,7 @@ class Library:
         M, K = x.shape
         F = out.shape[1]
         self.check(self.fn["SNEPPX_qlinear_w4a16_swiglu"](
-            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _ptr(bias), _ptr(out), M, F, K, group,
+            _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _bias_ptr(bias, 2 * F, out), _ptr(out), M, F, K, group,
             self._stream(stream)), "qlinear_w4a16_swiglu")
 
     def qlinear_silu_mul(self, gate_up, out, stream=None):
@@ -402,7 +424,7 @@ class Library:
         M, K = A.shape
         N = W.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8a8_i8"](
-            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(bias), _ptr(out), M, N, K, self._stream(stream)),
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _bias_ptr(bias, N, out), _ptr(out), M, N, K, self._stream(stream)),
             "qlinear_w8a8_i8")
 
     def qlinear_i8_gemm_i32(self, A, W, Cm, stream=None):
@@ -415,7 +437,7 @@ class Library:
         M, K = A.shape
         N = W.shape[0]
         self.check(self.fn["SNEPPX_qlinear_w8a8_fp8"](
-            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _ptr(bias), _ptr(out), M, N, K, self._stream(stream)),
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _bias_ptr(bias, N, out), _ptr(out), M, N, K, self._stream(stream)),
             "qlinear_w8a8_fp8")
 
     # ---------------- model-zoo int8 (weights.c:225-252) -------------------
@@ -713,7 +735,9 @@ class QLayer:
             rc = self.L.fn["SNEPPX_qlayer_set_bias"](self.h, np.ascontiguousarray(bias, np.float32),
                                                       self.L._stream(stream))
         else:
-            rc = self.L.fn["SNEPPX_qlayer_set_bias_device"](self.h, _ptr(bias), self.L._stream(stream))
+            n = self.L.fn["SNEPPX_qlayer_out_features"](self.h)
+            rc = self.L.fn["SNEPPX_qlayer_set_bias_device"](self.h, _bias_ptr(bias, n, bias),
+                                                             self.L._stream(stream))
         self.L.check(rc, "qlayer_set_bias")
 
     def matmul_host(self, x):

@@ -1,9 +1,11 @@
 """The CPU oracle against the reference compiled unchanged (oracle/_ref), on
 seeded random and special-value inputs beyond the committed fixtures.
 
-Runs only where oracle/_ref/libsnxref.so was built (the build container,
-`make -C oracle ref`); the reference never travels to the GPU box, where the
-committed fixtures carry the same evidence."""
+Runs wherever oracle/_ref/libsnxref.so exists.  It is built from the
+reference's sources in the build container (`make -C oracle ref`), kept out
+of git history, and travels to the GPU box with the rest of the built
+libraries; the reference's source files never do.  Where the library is
+absent, the committed fixtures carry the same evidence."""
 import numpy as np
 import pytest
 
