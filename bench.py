@@ -36,8 +36,8 @@ FP6_PEAK_TFLOPS = 10066.3      # dense fp6 MFMA (MXFP6)
 # 2527-2553 TOPS after 300-3000 (one box, 200 timed launches each), so the
 # GEMM lines warm up for 300 launches (~30 ms) before their timed launches.
 GEMM_WARMUP, GEMM_STEPS = 300, 200
-MX_BENCH = {"mxfp4_e2m1": FP4_PEAK_TFLOPS, "mxfp8_e4m3": FP8_PEAK_TOPS, "mxfp8_e5m2": FP8_PEAK_TOPS,
-            "mxfp6_e3m2": FP6_PEAK_TFLOPS, "mxfp6_e2m3": FP6_PEAK_TFLOPS}
+MX_BENCH = {"mxfp4_e2m1": FP4_PEAK_TFLOPS, "nvfp4_e2m1": FP4_PEAK_TFLOPS, "mxfp8_e4m3": FP8_PEAK_TOPS,
+            "mxfp8_e5m2": FP8_PEAK_TOPS, "mxfp6_e3m2": FP6_PEAK_TFLOPS, "mxfp6_e2m3": FP6_PEAK_TFLOPS}
 SNEPPX_BFLOAT16 = 3            # SNEPPXDtype of include/sneppx_qlinear.h
 METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
 
@@ -387,8 +387,11 @@ def bench_mx(lib, timer, torch, M, N, K, steps, warmup, fmt="mxfp4_e2m1", mfma_f
     total, mean_launch, _ = timer.run([call], steps, warmup)
     flops = 2 * M * N * K
     rb = pa.shape[1] if pa.dim() == 2 else pa.numel() // M          # code bytes per row
-    host = {"pa": pa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(), "sa": sa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(),
-            "pw": pw.reshape(N, -1).cpu().numpy(), "sw": sw.reshape(N, -1).cpu().numpy(),
+    per_tensor = sa.numel() == 1                                     # NVFP4: one exponent per operand
+    host = {"pa": pa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(),
+            "sa": sa.reshape(-1).cpu().numpy() if per_tensor else sa.reshape(M, -1)[:CPU_ROWS].cpu().numpy(),
+            "pw": pw.reshape(N, -1).cpu().numpy(),
+            "sw": sw.reshape(-1).cpu().numpy() if per_tensor else sw.reshape(N, -1).cpu().numpy(),
             "M": M, "N": N, "K": K, "fmt": fmt, "flops": flops, "row_bytes": rb}
     return {"ms_per_step": total / steps, "tflops": flops / (total / steps) / 1e9,
             "tflops_kernel": flops / mean_launch / 1e9, "host": host}
@@ -682,7 +685,8 @@ def cpu_legs(orc, jobs, seconds):
             nw = min(N, 512)                   # rows of W decoded (the numpy bit unpack is slow)
             with threadpool_limits(limits=1):
                 t0 = time.perf_counter()
-                wd = mx_oracle.dequantize(h["pw"][:nw].reshape(-1), h["sw"][:nw].reshape(-1), (nw, K),
+                sw_rows = h["sw"] if h["sw"].size == 1 else h["sw"][:nw]     # per-tensor NVFP4: one exponent
+                wd = mx_oracle.dequantize(h["pw"][:nw].reshape(-1), sw_rows.reshape(-1), (nw, K),
                                           fmt).astype(np.float32)
                 t_w = time.perf_counter() - t0
                 t0 = time.perf_counter()
@@ -961,6 +965,7 @@ def main():
                 r = bench_mx(lib, timer, torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP, fmt, mfma_form=kept)
                 how = ("operands kept in matrix-core form" if kept else
                        "both operands converted every call" if fmt.startswith("mxfp8") else
+                       "per-tensor exponents fed to every 32-block" if fmt.startswith("nvfp4") else
                        "reference MX encoding")
                 extra.append({"workload": f"{fmt.upper()} GEMM M=2048 N=14336 K=4096 ({how}, bf16 out)",
                               "value": round(r["tflops"], 1), "unit": "TFLOP/s",

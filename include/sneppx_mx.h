@@ -79,9 +79,11 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
                               const int8_t* sW, void* out, SNEPPXDtype out_dtype, size_t M,
                               size_t N, size_t K, SNEPPXStream stream);
 
-/* The same linear for every block-32 MX format (no reference counterpart):
+/* The same linear for every MX format (no reference counterpart):
  * A [M][K] and W [N][K] both in `fmt` (MXFP8 E4M3 / E5M2, MXFP6 E3M2 / E2M3,
- * MXFP4), as SNEPPX_dev_quantize_mx writes them with the default block;
+ * MXFP4, and NVFP4 with its per-tensor exponent, sA / sW one int8 each, as
+ * SNEPPX_qlinear_mx_gemm_bs with block 0), as SNEPPX_dev_quantize_mx writes
+ * them with the default block;
  * out bf16 or fp32 [M][N], fp32 accumulation on the scaled f8f6f4 matrix
  * cores (the block exponents go in as their E8M0 scales).  FP6 and FP4 codes
  * are the matrix cores' own.  The reference's FP8 codes with an all-ones
@@ -95,6 +97,22 @@ int SNEPPX_qlinear_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t*
 int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                            SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype, size_t M,
                            size_t N, size_t K, SNEPPXStream stream);
+
+/* SNEPPX_qlinear_mx_gemm for operands quantized with any block the
+ * matrix cores can scale exactly (no reference counterpart; the block rule
+ * is SNEPPX_dev_quantize_mx's, mx_formats.py:147-150,165): block_size 0 is
+ * the format's default (32, or per tensor for NVFP4), a negative one per
+ * tensor, a positive one a multiple of 32 dividing K.  Per tensor, sA and sW
+ * are one int8 each and every 32-element block takes them as its scales
+ * (mx_formats.py:165-172, 199-203); a block of 32 r repeats each exponent for
+ * its r pieces of 32.  Blocks that are no multiple of 32 (e.g. 16) return -1:
+ * the matrix cores scale 32 elements with one exponent.  NVFP4 runs the
+ * MXFP4 kernels (the same E2M1 codes).  The rewritten exponents go to the
+ * calling thread's workspace (M + N rows of K/32 bytes). */
+int SNEPPX_qlinear_mx_gemm_bs(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                              const int8_t* sW, SNEPPXMXFormat fmt, int block_size, void* out,
+                              SNEPPXDtype out_dtype, size_t M, size_t N, size_t K,
+                              SNEPPXStream stream);
 
 /* Reference MX codes of a [rows][cols] block-32 tensor -> codes and
  * exponents the matrix cores decode to the same values (no reference

@@ -349,6 +349,38 @@ __global__ void __launch_bounds__(256) k_mx_to_mfma(const uint8_t* __restrict__ 
     if (inexact && rounded) atomicAdd(rounded, (unsigned)inexact);
 }
 
+// Exponents of one GEMM operand in the block-32 form the matrix-core GEMMs
+// read (one int8 per 32 elements of a row: the matrix cores scale 32-element
+// blocks).  rep > 0: a blocked tensor whose block is 32 * rep elements, each
+// exponent repeated for its rep 32-element pieces.  rep == 0: a per-tensor
+// exponent (NVFP4), where the product's exponent t = sA + sW is what
+// matters; A takes ceil(t / 2) and W floor(t / 2) (which = 0 / 1), so that
+// neither reaches -128, which the E8M0 conversion clamps to 2^-127 (at
+// t < -254 both halves clamp to -127, and every product then underflows to
+// zero in fp32 as it does at the exact exponent).
+__global__ void __launch_bounds__(256) k_mx_expand_scales(const int8_t* __restrict__ src,
+                                                          const int8_t* __restrict__ sA,
+                                                          const int8_t* __restrict__ sW,
+                                                          int8_t* __restrict__ dst, size_t rows,
+                                                          uint32_t kb32, uint32_t rep, int which) {
+    const size_t n = rows * kb32;
+    int pt = 0;
+    if (rep == 0) {
+        const int t = (int)sA[0] + (int)sW[0];
+        const int hi = t - (t >> 1), lo = t >> 1;          // ceil, floor (arithmetic shift)
+        pt = which == 0 ? hi : lo;
+        pt = pt < -127 ? -127 : pt;
+    }
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+        if (rep == 0) {
+            dst[i] = (int8_t)pt;
+        } else {
+            const size_t r = i / kb32, c = i % kb32;
+            dst[i] = src[r * (kb32 / rep) + c / rep];
+        }
+    }
+}
+
 }  // namespace
 
 extern "C" {
@@ -394,6 +426,17 @@ int snx_k_mx_quant_tensor(const float* x, uint8_t* packed, size_t n, int s, int 
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* st) {
     k_mx_dequant_tensor<<<grid_of(n), 256, 0, S(st)>>>(packed, y, n, s, f);
     return snx_launch_check("k_mx_dequant_tensor");
+}
+
+int snx_k_mx_expand_scales(const int8_t* src, const int8_t* sA, const int8_t* sW, int8_t* dst,
+                           size_t rows, size_t kb32, unsigned rep, int which, void* st) {
+    if (kb32 == 0 || kb32 > 0xffffffffu || (rep && kb32 % rep)) {
+        snx_set_error("mx scales: %zu blocks of 32 per row do not split into blocks of %u", kb32, 32 * rep);
+        return -1;
+    }
+    k_mx_expand_scales<<<grid_of(rows * kb32), 256, 0, S(st)>>>(src, sA, sW, dst, rows, (uint32_t)kb32, rep,
+                                                                which);
+    return snx_launch_check("k_mx_expand_scales");
 }
 
 int snx_k_mx_to_mfma(const uint8_t* in, const int8_t* sin, uint8_t* out, int8_t* sout,

@@ -199,6 +199,8 @@ int SNEPPX_qlinear_mx_gemm_mfma(const uint8_t* A, const int8_t* sA, const uint8_
 int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                            SNEPPXMXFormat fmt, void* out, SNEPPXDtype out_dtype, size_t M,
                            size_t N, size_t K, SNEPPXStream stream) {
+    if (fmt == SNEPPX_NVFP4_E2M1)   /* per tensor by default (mx_formats.py:72-73) */
+        return SNEPPX_qlinear_mx_gemm_bs(A, sA, W, sW, fmt, 0, out, out_dtype, M, N, K, stream);
     if (mx_gemm_check("qlinear_mx_gemm", A, sA, W, sW, fmt, out, out_dtype, M, N, K)) return -1;
     snx_clear_error();
     if (fmt != SNEPPX_MXFP8_E4M3 && fmt != SNEPPX_MXFP8_E5M2)
@@ -216,5 +218,42 @@ int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
     if (!rc) rc = SNEPPX_mx_to_mfma(W, sW, w2, sw2, N, K, fmt, NULL, stream);
     if (!rc) rc = snx_k_mx8_gemm(a2, sa2, w2, sw2, out, out_dtype == SNEPPX_FLOAT32, mfma_fmt(fmt), M, N,
                                  K, stream);
+    return rc;
+}
+
+/* Any block the reference's quantize_mx takes (mx_formats.py:147-150: the
+ * format's own, an override, or per tensor) whose scales the matrix cores
+ * can apply exactly: per tensor, or a multiple of 32 elements.  The
+ * exponents are rewritten into the block-32 form (k_mx_expand_scales, into
+ * the calling thread's workspace) and the block-32 GEMM runs on the
+ * operands' own codes: NVFP4's and MXFP4's E2M1 codes are the same, and with
+ * K a multiple of the block every row's codes start on a byte. */
+int SNEPPX_qlinear_mx_gemm_bs(const uint8_t* A, const int8_t* sA, const uint8_t* W,
+                              const int8_t* sW, SNEPPXMXFormat fmt, int block_size, void* out,
+                              SNEPPXDtype out_dtype, size_t M, size_t N, size_t K,
+                              SNEPPXStream stream) {
+    static const char* who = "qlinear_mx_gemm_bs";
+    REQUIRE(valid_fmt(fmt), "%s: unknown format %d", who, (int)fmt);
+    const int bs = block_of(fmt, block_size);
+    REQUIRE(bs >= 0, "%s: block size %d must be a positive multiple of 8, 0 or -1", who, block_size);
+    REQUIRE(bs == 0 || bs % 32 == 0,
+            "%s: block %d: the matrix cores scale blocks of 32 elements, so a block must be per "
+            "tensor or a multiple of 32", who, bs);
+    REQUIRE(bs == 0 || K % (size_t)bs == 0, "%s: K=%zu must be a multiple of the block (%d)", who, K, bs);
+    const SNEPPXMXFormat ef = fmt == SNEPPX_NVFP4_E2M1 ? SNEPPX_MXFP4_E2M1 : fmt;   /* element format */
+    if (bs == 32) return SNEPPX_qlinear_mx_gemm(A, sA, W, sW, ef, out, out_dtype, M, N, K, stream);
+    REQUIRE(A && sA && W && sW && out, "%s: NULL pointer", who);
+    REQUIRE(M && N && K, "%s: empty shape", who);
+    REQUIRE(K % 32 == 0, "%s: K=%zu must be a multiple of 32", who, K);
+    snx_clear_error();
+    const size_t kb = K / 32, ab = (M * kb + 255) & ~(size_t)255;
+    int8_t* ws = (int8_t*)snx_workspace(ab + N * kb, 1, stream);
+    if (!ws) return -1;
+    int8_t* sa32 = ws;
+    int8_t* sw32 = ws + ab;
+    const unsigned rep = (unsigned)(bs / 32);
+    int rc = snx_k_mx_expand_scales(sA, sA, sW, sa32, M, kb, rep, 0, stream);
+    if (!rc) rc = snx_k_mx_expand_scales(sW, sA, sW, sw32, N, kb, rep, 1, stream);
+    if (!rc) rc = SNEPPX_qlinear_mx_gemm(A, sa32, W, sw32, ef, out, out_dtype, M, N, K, stream);
     return rc;
 }

@@ -89,6 +89,11 @@ int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W,
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* stream);
 /* reference MXFP8 blocks (f 0 e4m3, 1 e5m2) -> matrix-core-decodable codes and
  * exponents; *rounded (device, may be NULL) counts elements that rounded */
+/* block-32 exponents of a GEMM operand from a block of 32 * rep (rep > 0) or
+ * a per-tensor exponent (rep == 0: operand `which` 0 = A / 1 = W takes its
+ * share of sA[0] + sW[0]) */
+int snx_k_mx_expand_scales(const int8_t* src, const int8_t* sA, const int8_t* sW, int8_t* dst,
+                           size_t rows, size_t kb32, unsigned rep, int which, void* stream);
 int snx_k_mx_to_mfma(const uint8_t* in, const int8_t* sin, uint8_t* out, int8_t* sout,
                      size_t nblocks, int f, unsigned int* rounded, void* stream);
 /* MXFP8 / MXFP6 GEMM on matrix-core-decodable operands; mf the MFMA element

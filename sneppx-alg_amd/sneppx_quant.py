@@ -136,6 +136,8 @@ EXPORTS = {
     "SNEPPX_qlinear_mxfp4_gemm": (C.c_int, [_vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_mx_gemm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _sz, _sz, _sz, _vp]),
     "SNEPPX_qlinear_mx_gemm_mfma": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, _vp, C.c_int, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_mx_gemm_bs": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, _vp, C.c_int, _sz, _sz, _sz,
+                                            _vp]),
     "SNEPPX_mx_to_mfma": (C.c_int, [_vp, _vp, _vp, _vp, _sz, _sz, C.c_int, _vp, _vp]),
     # thin HIP ABI
     "snx_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
@@ -536,6 +538,14 @@ class Library:
         self.check(self.fn[name](
             _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), MX_FORMATS.index(fmt), _ptr(out), ydt, M, N, K,
             self._stream(stream)), name[7:])
+
+    def qlinear_mx_gemm_bs(self, A, sA, W, sW, fmt, out, M, N, K, block_size=None, stream=None):
+        """out = A W^T for MX operands quantized with `block_size` (the rule of
+        dev_quantize_mx: None = the format's default, <= 0 per tensor)."""
+        ydt = SNEPPX_FLOAT32 if out.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_mx_gemm_bs"](
+            _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), MX_FORMATS.index(fmt), self._mx_block(fmt, block_size),
+            _ptr(out), ydt, M, N, K, self._stream(stream)), "qlinear_mx_gemm_bs")
 
     def mx_to_mfma(self, packed, scales, rows, cols, fmt, stream=None):
         """(packed, scales, rounded) in the matrix cores' encoding; rounded is an

@@ -215,5 +215,144 @@ def test_mx_gemm_rejects_bad_shapes(lib):
     y = torch.empty((2, 2), device=DEV)
     with pytest.raises(Exception, match="multiple of 128"):
         lib.qlinear_mx_gemm(z, s, z, s, "mxfp8_e4m3", y, 2, 2, 96)
-    with pytest.raises(Exception, match="block-32"):
-        lib.qlinear_mx_gemm(z, s, z, s, "nvfp4_e2m1", y, 2, 2, 128)
+    # blocks the matrix cores cannot scale exactly (not a multiple of 32)
+    with pytest.raises(Exception, match="blocks of 32"):
+        lib.qlinear_mx_gemm_bs(z, s, z, s, "mxfp4_e2m1", y, 2, 2, 128, block_size=16)
+    with pytest.raises(Exception, match="multiple of the block"):
+        lib.qlinear_mx_gemm_bs(z, s, z, s, "mxfp4_e2m1", y, 2, 2, 192, block_size=128)
+
+
+def _expanded(scales, rows, K, bs, fmt):
+    """block-32 exponents [rows][K/32] of an operand quantized with block bs
+    (None: the format's default; per tensor when <= 0): what the GEMM's scale
+    expansion stands for."""
+    s = np.asarray(scales, np.int64).reshape(-1)
+    if bs is None:
+        bs = mx.SPECS[fmt].block_size
+    if bs <= 0:
+        return np.full((rows, K // 32), s[0], np.int64)
+    return np.repeat(s.reshape(rows, K // bs), bs // 32, axis=1)
+
+
+def _values(packed, scales, rows, K, fmt, bs):
+    """float64 matrix-core values of an operand: its block-32 exponents, the
+    FP8 codes through the oracle's re-encoding (exact but for the counted
+    half-to-even elements), FP6 / FP4 as the reference decodes them."""
+    ef = "mxfp4_e2m1" if fmt == "nvfp4_e2m1" else fmt
+    s32 = _expanded(scales, rows, K, bs, fmt)
+    if mx.SPECS[ef].bits == 8:
+        return _mfma_values(np.asarray(packed).reshape(-1), s32.astype(np.int8), rows, K, ef)
+    return mx.dequantize(np.asarray(packed).reshape(-1), s32.astype(np.int8), (rows, K), ef).astype(np.float64)
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 224, 256), (300, 500, 512), (1, 17, 128), (2048, 1024, 1024)])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_nvfp4_gemm_against_dequantized_product(lib, M, N, K, out):
+    """NVFP4 (E2M1 codes, one per-tensor exponent each, mx_formats.py:72-73,
+    165-172) through the E2M1 matrix-core kernels against the float64
+    product of the reference's dequantized operands."""
+    print(f"[gpu] nvfp4 gemm M={M} N={N} K={K} {out}", flush=True)
+    rng = np.random.default_rng(M * 7 + N + K)
+    a = rng.normal(0, 1, (M, K)).astype(np.float32)
+    w = (rng.normal(0, 0.02, (N, K))).astype(np.float32)
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(a).to(DEV), "nvfp4_e2m1")
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(w).to(DEV), "nvfp4_e2m1")
+    assert sa.numel() == 1 and sw.numel() == 1
+    y = torch.empty((M, N), dtype=torch.float32 if out == "f32" else torch.bfloat16, device=DEV)
+    lib.qlinear_mx_gemm(pa, sa, pw, sw, "nvfp4_e2m1", y, M, N, K)
+    torch.cuda.synchronize()
+    da = mx.dequantize(pa.cpu().numpy(), sa.cpu().numpy(), (M, K), "nvfp4_e2m1").astype(np.float64)
+    dw = mx.dequantize(pw.cpu().numpy(), sw.cpu().numpy(), (N, K), "nvfp4_e2m1").astype(np.float64)
+    ref = da @ dw.T
+    got = y.float().cpu().numpy().astype(np.float64)
+    err = np.abs(got - ref).max() / np.abs(ref).max()
+    assert err <= (1e-5 if out == "f32" else 1e-2), err
+
+
+def test_nvfp4_gemm_extreme_exponents(lib):
+    """An operand whose per-tensor exponent is -128 (peak just above FLT_MIN)
+    against one near 2^100: the product's exponent is split between the two
+    E8M0 scales, so neither is clamped (clamping -128 to -127 would double
+    every output)."""
+    print("[gpu] nvfp4 gemm extreme exponents", flush=True)
+    rng = np.random.default_rng(31)
+    M, N, K = 130, 260, 512
+    a = (rng.uniform(-1, 1, (M, K)) * 1.7e-38).astype(np.float32)
+    a[0, 0] = 1.7e-38
+    w = (rng.normal(0, 1, (N, K)) * 2.0 ** 100).astype(np.float32)
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(a).to(DEV), "nvfp4_e2m1")
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(w).to(DEV), "nvfp4_e2m1")
+    assert int(sa.cpu()[0]) == -128 and int(sw.cpu()[0]) > 90
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_mx_gemm(pa, sa, pw, sw, "nvfp4_e2m1", y, M, N, K)
+    torch.cuda.synchronize()
+    da = mx.dequantize(pa.cpu().numpy(), sa.cpu().numpy(), (M, K), "nvfp4_e2m1").astype(np.float64)
+    dw = mx.dequantize(pw.cpu().numpy(), sw.cpu().numpy(), (N, K), "nvfp4_e2m1").astype(np.float64)
+    ref = da @ dw.T
+    got = y.cpu().numpy().astype(np.float64)
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("fmt,bs", [("mxfp4_e2m1", 64), ("mxfp4_e2m1", -1), ("mxfp8_e4m3", 128),
+                                    ("mxfp8_e5m2", -1), ("mxfp6_e3m2", 64), ("mxfp6_e2m3", -1),
+                                    ("nvfp4_e2m1", 32), ("nvfp4_e2m1", 256)])
+def test_mx_gemm_other_blocks(lib, fmt, bs):
+    """Operands quantized with a block override or per tensor (the
+    reference's block_size argument, mx_formats.py:147-150,165) against the
+    float64 product of their matrix-core values."""
+    print(f"[gpu] mx gemm {fmt} block {bs}", flush=True)
+    rng = np.random.default_rng(abs(bs) + len(fmt))
+    M, N, K = 300, 260, 1024
+    a, w = _mx_operand(rng, M, K, 1), _mx_operand(rng, N, K, 1) * 0.02
+    pa, sa = lib.dev_quantize_mx(torch.from_numpy(a).to(DEV), fmt, bs)
+    pw, sw = lib.dev_quantize_mx(torch.from_numpy(w).to(DEV), fmt, bs)
+    y = torch.empty((M, N), device=DEV)
+    lib.qlinear_mx_gemm_bs(pa, sa.reshape(-1), pw, sw.reshape(-1), fmt, y, M, N, K, block_size=bs)
+    torch.cuda.synchronize()
+    hpa, hsa, hpw, hsw = (t.cpu().numpy() for t in (pa, sa, pw, sw))
+    va, vw = _values(hpa, hsa, M, K, fmt, bs), _values(hpw, hsw, N, K, fmt, bs)
+    ref = va @ vw.T
+    got = y.cpu().numpy().astype(np.float64)
+    absprod = np.abs(va) @ np.abs(vw).T
+    assert (np.abs(got - ref) / np.maximum(absprod, 1e-300)).max() <= 2.0 ** -13
+    refd = mx.dequantize(hpa, hsa, (M, K), fmt, bs) @ mx.dequantize(hpw, hsw, (N, K), fmt, bs).T
+    assert np.abs(ref - refd).max() <= 1e-6 * np.abs(refd).max()
+
+
+@pytest.mark.parametrize("fmt", ["mxfp4_e2m1", "nvfp4_e2m1", "mxfp8_e4m3", "mxfp6_e3m2", "mxfp6_e2m3"])
+def test_mx_gemm_full_c4_shape_sampled(lib, fmt):
+    """The bench's 2048 x 14336 x 4096 MX GEMMs (bf16 out): the four corner
+    and eight random 64 x 64 output tiles against the float64 product of the
+    matrix-core values of those rows and columns (tolerance 1e-2 of the
+    tile's largest output)."""
+    print(f"[gpu] mx gemm {fmt} 2048x14336x4096 sampled", flush=True)
+    M, N, K = 2048, 14336, 4096
+    g = torch.Generator(device=DEV).manual_seed(19)
+    a = torch.randn((M, K), device=DEV, generator=g)
+    w = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    pa, sa = lib.dev_quantize_mx(a, fmt)
+    pw, sw = lib.dev_quantize_mx(w, fmt)
+    del a, w
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    lib.qlinear_mx_gemm(pa, sa.reshape(-1), pw, sw.reshape(-1), fmt, y, M, N, K)
+    torch.cuda.synchronize()
+    rb = K * mx.SPECS["mxfp4_e2m1" if fmt == "nvfp4_e2m1" else fmt].bits // 8
+    hpa, hpw = pa.reshape(M, rb).cpu().numpy(), pw.reshape(N, rb).cpu().numpy()
+    hsa, hsw = sa.cpu().numpy().reshape(-1), sw.cpu().numpy().reshape(-1)
+    bs = None if fmt == "nvfp4_e2m1" else 32
+    rng = np.random.default_rng(5)
+    tiles = [(0, 0), (M - 64, 0), (0, N - 64), (M - 64, N - 64)] + \
+        [(int(rng.integers(0, M // 64)) * 64, int(rng.integers(0, N // 64)) * 64) for _ in range(8)]
+    got_all = y.float()
+    for m0, n0 in tiles:
+        if fmt == "nvfp4_e2m1":
+            ssa, ssw = hsa, hsw
+        else:
+            ssa = hsa.reshape(M, K // 32)[m0:m0 + 64].ravel()
+            ssw = hsw.reshape(N, K // 32)[n0:n0 + 64].ravel()
+        va = _values(hpa[m0:m0 + 64].ravel(), ssa, 64, K, fmt, bs)
+        vw = _values(hpw[n0:n0 + 64].ravel(), ssw, 64, K, fmt, bs)
+        ref = va @ vw.T
+        got = got_all[m0:m0 + 64, n0:n0 + 64].cpu().numpy().astype(np.float64)
+        err = np.abs(got - ref).max() / np.abs(ref).max()
+        assert err <= 1e-2, (m0, n0, err)
