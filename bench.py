@@ -39,6 +39,8 @@ GEMM_WARMUP, GEMM_STEPS = 300, 200
 MX_BENCH = {"mxfp4_e2m1": FP4_PEAK_TFLOPS, "nvfp4_e2m1": FP4_PEAK_TFLOPS, "mxfp8_e4m3": FP8_PEAK_TOPS,
             "mxfp8_e5m2": FP8_PEAK_TOPS, "mxfp6_e3m2": FP6_PEAK_TFLOPS, "mxfp6_e2m3": FP6_PEAK_TFLOPS}
 SNEPPX_BFLOAT16 = 3            # SNEPPXDtype of include/sneppx_qlinear.h
+GRAPH_HOLD_CYCLES = 400_000    # GPU spin (~0.2 ms) ahead of a timed graph replay
+DECODE_GRAPH = False           # time the decode GEMV lines as one HIP graph replay (--graph)
 METRIC = "W4A16 GEMV achieved HBM GB/s (% peak); W8A8 GEMM TOPS at M=2048 (% peak)"
 
 
@@ -52,6 +54,7 @@ def parse():
     p.add_argument("--no-extra", action="store_true", help="headline config only")
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
+    p.add_argument("--graph", action="store_true", help="--only: time the decode lines as a HIP graph replay")
     p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "decode", "shard", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
@@ -66,37 +69,60 @@ def w4_bytes(M, N, K, G, zeros=True, gidx=False):
     return b
 
 
+def _graph(graph):
+    """A decode bench's timing mode: its own argument, else --graph."""
+    return DECODE_GRAPH if graph is None else graph
+
+
 class Timer:
     """HIP events recorded on the stream the kernels are launched on."""
 
     def __init__(self, lib, stream):
         self.lib, self.stream = lib, stream
 
-    def run(self, calls, steps, warmup, loop=None):
+    def run(self, calls, steps, warmup, loop=None, graph=False):
         """Back-to-back time of `steps` calls between two events; `loop(n)`,
-        when given, issues n calls from C (bench_loop.c) instead of Python."""
+        when given, issues n calls from C (bench_loop.c) instead of Python.
+        graph: the `steps` calls are captured once into a HIP graph and the
+        timed region is one replay of it (one host call for the whole run,
+        as a decode loop runs its captured steps), the calls' own kernels
+        back to back on the GPU."""
         import torch
+
+        def issue(n):
+            if loop:
+                loop(n)
+            else:
+                for i in range(n):
+                    calls[i % len(calls)]()
         a, b = self.lib.event(), self.lib.event()
+        g = None
+        if graph:
+            issue(1)                   # any workspace exists before the capture
+            torch.cuda.synchronize()
+            g = self.lib.capture(lambda: issue(steps), self.stream)
         torch.cuda.synchronize()
-        if loop:
-            loop(warmup)
-        else:
-            for i in range(warmup):
-                calls[i % len(calls)]()
+        issue(warmup)
+        if g is not None:
+            self.lib.graph_launch(g, self.stream)     # untimed replay: the graph's first upload
+            # a bounded spin on the GPU keeps the queue busy while the host
+            # submits the timed replay, so its first kernel follows at once
+            torch.cuda._sleep(GRAPH_HOLD_CYCLES)
         # whole-job time: back-to-back launches between two events.  The
         # start event is queued right behind the warm-up launches (no host
         # synchronisation in between), so the timed launches begin on a busy
         # queue: the first launch's wake-up latency stays in the warm-up and
         # a short run times the same steady state as a long one.
         self.lib.record(a, self.stream)
-        if loop:
-            loop(steps)
+        if g is not None:
+            self.lib.graph_launch(g, self.stream)
         else:
-            for i in range(steps):
-                calls[i % len(calls)]()
+            issue(steps)
         self.lib.record(b, self.stream)
         torch.cuda.synchronize()
         total_ms = self.lib.elapsed_ms(a, b)
+        if g is not None:
+            self.lib.graph_destroy(g)
         # per-launch duration: an event pair around every launch
         evs = [(self.lib.event(), self.lib.event()) for _ in range(steps)]
         for i in range(steps):
@@ -175,7 +201,7 @@ def make_w4(lib, N, K, group, copies, seed, torch):
     return [(qw.clone(), sc.clone(), qz.clone()) for _ in range(copies)], G
 
 
-def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2):
+def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2, graph=None):
     ws, G = make_w4(lib, N, K, group, copies, seed, torch)
     g = torch.Generator(device="cuda").manual_seed(seed + 1)
     x = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
@@ -186,7 +212,7 @@ def bench_w4a16(lib, timer, torch, M, N, K, group, copies, steps, warmup, seed=2
     qwa, sca, qza = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws]), ptr_array([c[2] for c in ws])
     loop = make_loop("snxb_loop_w4a16", C.c_int(len(ws)), x, qwa, sca, qza, y, C.c_int(SNEPPX_BFLOAT16),
                      M, N, K, C.c_int(group), C.c_void_p(st))
-    total, mean_launch, med_launch = timer.run(calls, steps, warmup, loop)
+    total, mean_launch, med_launch = timer.run(calls, steps, warmup, loop, graph=_graph(graph))
     nbytes = w4_bytes(M, N, K, G)
     return {
         "bytes": nbytes, "ms_per_step": total / steps, "launch_ms_mean": mean_launch,
@@ -206,7 +232,7 @@ def llama_linears(tp=1):
             "down": (4096, 14336 // tp)}
 
 
-def bench_decode(lib, timer, torch, copies, steps, warmup, layer, tp=1):
+def bench_decode(lib, timer, torch, copies, steps, warmup, layer, tp=1, graph=None):
     """One token (M = 1) through C5's Llama-3-8B linears: the gate/up
     projection with its SwiGLU step as one launch (layer False), or the
     layer's four linears back to back (QKV, O, gate/up + SwiGLU, down; the
@@ -247,7 +273,7 @@ def bench_decode(lib, timer, torch, copies, steps, warmup, layer, tp=1):
             calls.append(bound(lib, "SNEPPX_qlinear_w4a16", bufs["h"], d[0], d[1], d[2], None, 0, None,
                                bufs["y"], SNEPPX_BFLOAT16, 1, H, F, 128, C.c_void_p(st)))
         return lambda: [f() for f in calls]
-    total, mean_step, _ = timer.run([step(c) for c in range(copies)], steps, warmup, loop)
+    total, mean_step, _ = timer.run([step(c) for c in range(copies)], steps, warmup, loop, graph=_graph(graph))
     nbytes = sum(w4_bytes(1, N, K, K // 128) for n, (N, K) in shapes.items() if n in names)
     nbytes -= 2 * F if "gate_up" in names else 0        # gate/up writes F outputs, not 2 F
     host = {n: tuple(t.cpu() for t in ws[n][0]) for n in names}
@@ -255,7 +281,7 @@ def bench_decode(lib, timer, torch, copies, steps, warmup, layer, tp=1):
             "host": {"w": host, "x": _u16(x), "shapes": shapes}}
 
 
-def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
+def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup, graph=None):
     """C3: GPTQ act-order weights, prepared once into group-contiguous column
     order (SNEPPX_qlinear_w4_actorder_prepare), then the decode linear that
     gathers the activations by the permutation."""
@@ -282,14 +308,14 @@ def bench_w4a16_gptq(lib, timer, torch, M, N, K, copies, steps, warmup):
     qwa, sca = ptr_array([c[0] for c in ws]), ptr_array([c[1] for c in ws])
     loop = make_loop("snxb_loop_w4a16_actorder", C.c_int(len(ws)), x, qwa, sca, order, y,
                      C.c_int(SNEPPX_BFLOAT16), M, N, K, C.c_int(128), C.c_void_p(st))
-    total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
+    total, mean_launch, _ = timer.run(calls, steps, warmup, loop, graph=_graph(graph))
     nbytes = w4_bytes(M, N, K, G, zeros=False) + K * 2      # + uint16 perm
     host["x"] = _u16(x)
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
             "gbs_kernel": nbytes / mean_launch / 1e6, "host": host}
 
 
-def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
+def bench_w8(lib, timer, torch, N, K, copies, steps, warmup, graph=None):
     g = torch.Generator(device="cuda").manual_seed(11)
     w = torch.randn((N, K), device="cuda", generator=g) * 0.02
     q = torch.empty((N, K), dtype=torch.int8, device="cuda")
@@ -310,7 +336,7 @@ def bench_w8(lib, timer, torch, N, K, copies, steps, warmup):
              for c in ws]
     loop = make_loop("snxb_loop_w8_gemv", C.c_int(len(ws)), x, ptr_array([c[0] for c in ws]),
                      ptr_array([c[1] for c in ws]), y, 1, N, K, C.c_void_p(st))
-    total, mean_launch, _ = timer.run(calls, steps, warmup, loop)
+    total, mean_launch, _ = timer.run(calls, steps, warmup, loop, graph=_graph(graph))
     nbytes = N * K + N * 4 + K * 4 + N * 4
     host = {"q": q.cpu().numpy(), "s": s.cpu().numpy(), "x": x.cpu().numpy()}
     return {"bytes": nbytes, "ms_per_step": total / steps, "gbs": nbytes / (total / steps) / 1e6,
@@ -361,6 +387,31 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
             "sW": sW.cpu().numpy(), "M": M}
     return {"ops": ops, "ms_per_step": total / steps, "tops": ops / (total / steps) / 1e9,
             "tops_kernel": ops / mean_launch / 1e9, "host": host}
+
+
+def bench_w8a8_dyn(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
+    """C4 as a layer runs it: bf16 activations in, quantized inside the timed
+    call (int8 per token / fp8 per tensor), the W8A8 GEMM, bf16 out."""
+    g = torch.Generator(device="cuda").manual_seed(13)
+    A = torch.randn((M, K), device="cuda", generator=g).to(torch.bfloat16)
+    w32 = torch.randn((N, K), device="cuda", generator=g) * 0.02
+    out = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
+    if fp8:
+        W = torch.empty((N, K), dtype=torch.uint8, device="cuda")
+        sW = torch.empty(1, device="cuda")
+        lib.dev_quantize_fp8_e4m3_scaled(w32, W, sW)
+    else:
+        W = torch.empty((N, K), dtype=torch.int8, device="cuda")
+        sW = torch.empty(N, device="cuda")
+        lib.dev_quantize_int8_channel(w32, W, sW)
+    del w32
+    st = timer.stream
+    Ab = A.view(torch.int16)
+    total, mean_launch, _ = timer.run([lambda: lib.qlinear_w8a8_dyn(Ab, W, sW, out, fp8=fp8, stream=st)],
+                                      steps, warmup)
+    ops = 2 * M * N * K
+    return {"ops": ops, "ms_per_step": total / steps, "tops": ops / (total / steps) / 1e9,
+            "tops_kernel": ops / mean_launch / 1e9}
 
 
 def bench_mx(lib, timer, torch, M, N, K, steps, warmup, fmt="mxfp4_e2m1", mfma_form=False):
@@ -525,29 +576,40 @@ def bench_shards(lib, timer, torch, steps, warmup, tp=SHARD_TP, log=None):
     it.  Returns (extra entries, CPU jobs)."""
     out, jobs = [], []
     tag = f"TP={tp} shard: "
+    # The shard's decode kernels (0.7-8 MB, 3-4 us) are shorter than the
+    # host's ~3 us launch path, so launched one by one they time the host.
+    # A decode loop runs such steps as a captured HIP graph: the value is one
+    # graph replay of the timed steps; the eager figure stays beside it.
+    how = " (HIP graph replay)"
+
+    def both(fn, *a, **kw):
+        r = fn(*a, graph=True, **kw)
+        r_eager = fn(*a, graph=False, **kw)
+        r0 = r_eager[0] if isinstance(r_eager, tuple) else r_eager
+        return r, round(r0["gbs"], 1)
     N2, K = 11008 // tp, 4096
     for m in (1, 16):
         cp = _copies_for(w4_bytes(m, N2, K, K // 128))
-        r, (ws_m, x_m, _, _) = bench_w4a16(lib, timer, torch, m, N2, K, 128, cp, steps, warmup)
-        out.append({"workload": f"{tag}C2 W4A16 g128 GEMV N={N2} K={K} M={m}", "value": round(r["gbs"], 1),
-                    "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+        (r, (ws_m, x_m, _, _)), eager = both(bench_w4a16, lib, timer, torch, m, N2, K, 128, cp, steps, warmup)
+        out.append({"workload": f"{tag}C2 W4A16 g128 GEMV N={N2} K={K} M={m}{how}", "value": round(r["gbs"], 1),
+                    "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "eager_gbs": eager,
                     "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
                     "weight_copies": cp})
         jobs.append((out[-1], "w4", {"qw": _u32(ws_m[0][0]), "sc": _u16(ws_m[0][1]), "qz": _u32(ws_m[0][2]),
                                      "x": _u16(x_m), "bytes": r["bytes"]}))
         del ws_m, x_m
     cp = _copies_for(w4_bytes(1, N2, K, K // 128, zeros=False))
-    r = bench_w4a16_gptq(lib, timer, torch, 1, N2, K, cp, steps, warmup)
-    out.append({"workload": f"{tag}C3 GPTQ act-order W4A16 (prepared) N={N2} K={K} M=1",
+    r, eager = both(bench_w4a16_gptq, lib, timer, torch, 1, N2, K, cp, steps, warmup)
+    out.append({"workload": f"{tag}C3 GPTQ act-order W4A16 (prepared) N={N2} K={K} M=1{how}",
                 "value": round(r["gbs"], 1), "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
-                "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
-                "weight_copies": cp})
+                "eager_gbs": eager, "kernel_gbs": round(r["gbs_kernel"], 1),
+                "ms_per_step": round(r["ms_per_step"], 5), "weight_copies": cp})
     jobs.append((out[-1], "w4_gidx", dict(r["host"], bytes=r["bytes"])))
     N1 = 4096 // tp
     cp = _copies_for(N1 * K)
-    r = bench_w8(lib, timer, torch, N1, K, cp, steps, warmup)
-    out.append({"workload": f"{tag}C1 W8 weight-only GEMV N={N1} K={K} M=1 fp32", "value": round(r["gbs"], 1),
-                "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4),
+    r, eager = both(bench_w8, lib, timer, torch, N1, K, cp, steps, warmup)
+    out.append({"workload": f"{tag}C1 W8 weight-only GEMV N={N1} K={K} M=1 fp32{how}", "value": round(r["gbs"], 1),
+                "unit": "GB/s", "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "eager_gbs": eager,
                 "kernel_gbs": round(r["gbs_kernel"], 1), "ms_per_step": round(r["ms_per_step"], 5),
                 "weight_copies": cp})
     jobs.append((out[-1], "w8", r["host"]))
@@ -555,13 +617,13 @@ def bench_shards(lib, timer, torch, steps, warmup, tp=SHARD_TP, log=None):
     for layer in (False, True):
         per_copy = sum(w4_bytes(1, N, K_, K_ // 128) for n, (N, K_) in sh.items() if layer or n == "gate_up")
         cp = _copies_for(per_copy)
-        r = bench_decode(lib, timer, torch, cp, steps, warmup, layer, tp=tp)
+        r, eager = both(bench_decode, lib, timer, torch, cp, steps, warmup, layer, tp=tp)
         what = ("Llama-3-8B layer linears at decode (QKV {qkv[0]}x{qkv[1]}, O {o[0]}x{o[1]}, gate/up "
                 "{gate_up[0]}x{gate_up[1]} + SwiGLU fused, down {down[0]}x{down[1]}; 4 launches)".format(**sh)
                 if layer else f"Llama-3-8B gate/up projection + SwiGLU fused, one launch "
                               f"(F={sh['gate_up'][0] // 2}, K={sh['gate_up'][1]})")
-        out.append({"workload": f"{tag}{what} W4A16 g128 M=1", "value": round(r["gbs"], 1), "unit": "GB/s",
-                    "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "bytes": r["bytes"],
+        out.append({"workload": f"{tag}{what} W4A16 g128 M=1{how}", "value": round(r["gbs"], 1), "unit": "GB/s",
+                    "frac_of_peak": round(r["gbs"] / HBM_PEAK_GBS, 4), "eager_gbs": eager, "bytes": r["bytes"],
                     "ms_per_step": round(r["ms_per_step"], 5), "weight_copies": cp})
         jobs.append((out[-1], "decode", dict(r["host"], bytes=r["bytes"], layer=layer)))
     r = bench_chain(lib, timer, torch, 10, 30, tp=tp)
@@ -884,11 +946,17 @@ def main():
         sys.exit(1)
     lib = sneppx_quant.load()
     arch, cus, clk = lib.device_info()
-    stream = torch.cuda.current_stream().cuda_stream
+    # one stream of our own (default priority) for every launch: a graph
+    # cannot be captured on the null stream
+    bench_stream = torch.cuda.Stream()
+    torch.cuda.set_stream(bench_stream)
+    stream = bench_stream.cuda_stream
     timer = Timer(lib, stream)
 
     N, K, group, M = 11008, 4096, 128, 1
     if args.only:
+        global DECODE_GRAPH
+        DECODE_GRAPH = args.graph
         run_only(args, lib, timer, torch, N, K, group)
         return
     head, keep = bench_w4a16(lib, timer, torch, M, N, K, group, args.copies, args.steps, args.warmup)
@@ -958,6 +1026,19 @@ def main():
             print(f"[bench] C4 W8A8 {kind} GEMM M=2048 N=14336 K=4096: {r['tops']:.0f} TOPS "
                   f"({r['tops'] / peak:.4f} of {peak:.0f}), {r['ms_per_step'] * 1e3:.1f} us/launch",
                   file=sys.stderr, flush=True)
+        for fp8 in (False, True):
+            r = bench_w8a8_dyn(lib, timer, torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP, fp8=fp8)
+            peak = FP8_PEAK_TOPS if fp8 else INT8_PEAK_TOPS
+            kind = "fp8" if fp8 else "int8"
+            rule = "per tensor" if fp8 else "per token"
+            extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} M=2048 N=14336 K=4096 from bf16 A "
+                                      f"(A quantized {rule} inside the timed call, bf16 out)",
+                          "value": round(r["tops"], 1), "unit": "TOPS", "frac_of_peak": round(r["tops"] / peak, 4),
+                          "ms_per_step": round(r["ms_per_step"], 4), "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
+            gemm[kind]["dyn_tops"] = r["tops"]
+            gemm[kind]["dyn_us"] = r["ms_per_step"] * 1e3
+            print(f"[bench] C4 W8A8 {kind} from bf16 A (quantized {rule} in the call): {r['tops']:.0f} TOPS "
+                  f"({r['tops'] / peak:.4f}), {r['ms_per_step'] * 1e3:.1f} us/call", file=sys.stderr, flush=True)
         torch.cuda.synchronize()
         extra.extend(bench_vendor_w8a8(torch, 2048, 14336, 4096, GEMM_STEPS, GEMM_WARMUP))
         for fmt, peak in MX_BENCH.items():
@@ -1038,6 +1119,9 @@ def main():
         line["roofline"][f"c4_{kind}_tops"] = round(g["tops"], 1)
         line["roofline"][f"c4_{kind}_frac"] = round(g["tops"] / g["peak"], 4)
         line["roofline"][f"c4_{kind}_us"] = round(g["ms_per_step"] * 1e3, 2)
+        if "dyn_tops" in g:
+            line["roofline"][f"c4_{kind}_bf16_in_tops"] = round(g["dyn_tops"], 1)
+            line["roofline"][f"c4_{kind}_bf16_in_frac"] = round(g["dyn_tops"] / g["peak"], 4)
         cb = g["line"].get("cpu_baseline") or {}
         if cb.get("value") is not None:
             line["cpu_baseline"] = dict(line["cpu_baseline"] or {})

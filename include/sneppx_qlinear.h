@@ -219,6 +219,23 @@ int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W,
                             const float* sW, const float* bias, uint16_t* out, size_t M,
                             size_t N, size_t K, SNEPPXStream stream);
 
+/* C4 with the activations quantized inside the call (no reference
+ * counterpart as one call): A bf16 [M][K] as it leaves the previous op, out
+ * bf16 [M][N].  int8: A per token with the rule of SNEPPX_quantize_int8_channel
+ * (quantize_int8.c:157-177) on each row of A, into a workspace (M*K bytes +
+ * M scales), then SNEPPX_qlinear_w8a8_i8 with W int8 [N][K] and per-channel
+ * sW [N].  fp8: A per tensor as SNEPPX_dev_quantize_fp8_e4m3_scaled (s_A =
+ * max|A|/240, codes e4m3(a / s_A)), then SNEPPX_qlinear_w8a8_fp8 with W's
+ * codes and its device scale sW.  Bit-identical to quantizing A with those
+ * entry points (on A converted to fp32, exact for bf16) and calling the
+ * GEMM. */
+int SNEPPX_qlinear_w8a8_i8_dyn(const uint16_t* A, const int8_t* W, const float* sW,
+                               const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                               SNEPPXStream stream);
+int SNEPPX_qlinear_w8a8_fp8_dyn(const uint16_t* A, const uint8_t* W, const float* sW,
+                                const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                                SNEPPXStream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -38,6 +38,19 @@ int snx_hip_event_elapsed_ms(float* ms, void* start, void* stop);
 /* Name of device 0's ISA ("gfx950:sramecc+:xnack-"), CU count and clock. */
 int snx_hip_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_khz);
 
+/* HIP graphs for launch-bound loops (a decode step's linears): every call
+ * made on `stream` between begin and end is recorded, not run (thread-local
+ * capture mode, so other threads' work is unaffected), and end returns an
+ * executable graph that graph_launch replays on a stream with one host call.
+ * The decode GEMVs take no workspace and record only kernel nodes (no
+ * memsets).  Entry points that allocate a workspace the first time they see
+ * a shape must have run once on that stream before capture, so that the
+ * workspace exists and the capture records kernels only. */
+int snx_hip_stream_begin_capture(void* stream);
+int snx_hip_stream_end_capture(void* stream, void** graph_exec);
+int snx_hip_graph_launch(void* graph_exec, void* stream);
+int snx_hip_graph_destroy(void* graph_exec);
+
 #ifdef __cplusplus
 }
 #endif

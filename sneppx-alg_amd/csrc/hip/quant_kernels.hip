@@ -61,12 +61,18 @@ __device__ float block_reduce(float v, F op, float* sh) {
 }
 
 // ---------------------------------------------------------------- reductions
-__global__ void k_absmax(const float* __restrict__ x, size_t n, float* __restrict__ part) {
+__device__ __forceinline__ float as_f32(float v) { return v; }
+__device__ __forceinline__ float as_f32(uint16_t v) {   // bf16 bits
+    return __builtin_bit_cast(float, (uint32_t)v << 16);
+}
+
+template <typename T = float>
+__global__ void k_absmax(const T* __restrict__ x, size_t n, float* __restrict__ part) {
     __shared__ float sh[16];
     float m = 0.0f;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x)
-        m = nanless_max(m, fabsf(x[i]));
+        m = nanless_max(m, fabsf(as_f32(x[i])));
     m = block_reduce(m, nanless_max, sh);
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
@@ -226,13 +232,13 @@ __global__ void k_dequant_int4_sym(const uint8_t* __restrict__ p, float* __restr
 // correctly rounded division, not x * (1/s): for s = amax/240 the quotient
 // puts the largest element at 240 (code 0x77) in about twice as many cases,
 // where the product's 239.99998 truncates to 224.
-template <int FMT>
-__global__ void k_fp8_encode(const float* __restrict__ x, uint8_t* __restrict__ c, size_t n,
+template <int FMT, typename T = float>
+__global__ void k_fp8_encode(const T* __restrict__ x, uint8_t* __restrict__ c, size_t n,
                              const float* __restrict__ rec) {
     float s = rec ? rec[0] : 1.0f;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n;
          i += (size_t)gridDim.x * blockDim.x) {
-        float v = rec ? x[i] / s : x[i];
+        float v = rec ? as_f32(x[i]) / s : as_f32(x[i]);
         c[i] = FMT == 0 ? fp8_e4m3_encode(v) : fp8_e5m2_encode(v);
     }
 }
@@ -268,6 +274,61 @@ __global__ void k_quant_int8_rows(const T* __restrict__ x, int8_t* __restrict__ 
             q[r * cols + c] = (int8_t)clampi(RNE ? rne_i32(v) : round_i32(v), -128, 127);
         }
         __syncthreads();
+    }
+}
+
+// Per-token int8 of bf16 activations, one pass: quantize_int8.c:157-177 on
+// each row (max|x| ignoring NaN, s = max/127 or 1 below FLT_MIN, code
+// clamp(roundf(x * (1/s)), -128, 127)), with the row held in registers -
+// one 256-thread block per row, CH 16-byte chunks (8 values) per thread, so
+// a row is read from memory once.  cols % 8 == 0, cols <= 2048 CH.
+typedef uint32_t u32x4q __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2q __attribute__((ext_vector_type(2)));
+template <int CH>
+__global__ void __launch_bounds__(256) k_quant_rows_bf16_reg(const uint16_t* __restrict__ x,
+                                                             int8_t* __restrict__ q,
+                                                             float* __restrict__ scales, size_t rows,
+                                                             int cols) {
+    __shared__ float sh[16];
+    const int nch = cols >> 3;
+    for (size_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint16_t* xr = x + r * (size_t)cols;
+        u32x4q v[CH];
+        float m = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int ch = threadIdx.x + 256 * c;
+            v[c] = ch < nch ? *reinterpret_cast<const u32x4q*>(xr + 8 * ch) : u32x4q{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                m = nanless_max(m, fabsf(__builtin_bit_cast(float, v[c][e] << 16)));
+                m = nanless_max(m, fabsf(__builtin_bit_cast(float, v[c][e] & 0xFFFF0000u)));
+            }
+        }
+        m = block_reduce(m, nanless_max, sh);
+        const float s = m < FLT_MIN ? 1.0f : m / 127.0f;
+        const float inv = 1.0f / s;
+        if (threadIdx.x == 0) scales[r] = s;
+#pragma unroll
+        for (int c = 0; c < CH; c++) {
+            const int ch = threadIdx.x + 256 * c;
+            if (ch >= nch) break;
+            u32x2q o;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                uint32_t w = 0u;
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const uint32_t b = v[c][2 * h + e];
+                    const int lo = clampi(round_i32(__builtin_bit_cast(float, b << 16) * inv), -128, 127);
+                    const int hi = clampi(round_i32(__builtin_bit_cast(float, b & 0xFFFF0000u) * inv), -128, 127);
+                    w |= ((uint32_t)(lo & 0xFF) | (uint32_t)(hi & 0xFF) << 8) << (16 * e);
+                }
+                o[h] = w;
+            }
+            *reinterpret_cast<u32x2q*>(q + r * (size_t)cols + 8 * ch) = o;
+        }
+        __syncthreads();   // sh is reused by the next row's reduction
     }
 }
 
@@ -714,6 +775,31 @@ int snx_k_quant_int8_rows_bf16(const uint16_t* x, int8_t* q, float* scales, size
     int grid = (int)(rows < 65536 ? rows : 65536);
     k_quant_int8_rows<false, uint16_t><<<grid, kBlock, 0, S(st)>>>(x, q, scales, rows, cols);
     return snx_launch_check("k_quant_int8_rows_bf16");
+}
+
+int snx_k_quant_rows_bf16_fast(const uint16_t* x, int8_t* q, float* scales, size_t rows, size_t cols,
+                               void* st) {
+    if (cols % 8 || cols > 8192 || ((uintptr_t)x & 15u) || ((uintptr_t)q & 7u))
+        return snx_k_quant_int8_rows_bf16(x, q, scales, rows, cols, st);
+    const int grid = (int)(rows < 65536 ? rows : 65536);
+    if (cols <= 2048)
+        k_quant_rows_bf16_reg<1><<<grid, 256, 0, S(st)>>>(x, q, scales, rows, (int)cols);
+    else if (cols <= 4096)
+        k_quant_rows_bf16_reg<2><<<grid, 256, 0, S(st)>>>(x, q, scales, rows, (int)cols);
+    else
+        k_quant_rows_bf16_reg<4><<<grid, 256, 0, S(st)>>>(x, q, scales, rows, (int)cols);
+    return snx_launch_check("k_quant_rows_bf16_reg");
+}
+
+int snx_k_absmax_bf16(const uint16_t* x, size_t n, float* part, int nparts, void* st) {
+    k_absmax<uint16_t><<<nparts, kBlock, 0, S(st)>>>(x, n, part);
+    return snx_launch_check("k_absmax_bf16");
+}
+
+int snx_k_fp8_encode_bf16(const uint16_t* x, uint8_t* c, size_t n, const float* rec, void* st) {
+    if (n == 0) return 0;
+    k_fp8_encode<0, uint16_t><<<grid_for(n, kBlock * 4), kBlock, 0, S(st)>>>(x, c, n, rec);
+    return snx_launch_check("k_fp8_encode_bf16");
 }
 
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* st) {

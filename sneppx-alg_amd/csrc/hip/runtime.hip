@@ -219,4 +219,31 @@ int snx_hip_device_info(char* arch, size_t arch_len, int* cu_count, int* clock_k
     return 0;
 }
 
+int snx_hip_stream_begin_capture(void* stream) {
+    return check(hipStreamBeginCapture(S(stream), hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+}
+
+int snx_hip_stream_end_capture(void* stream, void** graph_exec) {
+    if (!graph_exec) return -1;
+    *graph_exec = nullptr;
+    hipGraph_t g = nullptr;
+    if (check(hipStreamEndCapture(S(stream), &g), "hipStreamEndCapture")) return -1;
+    hipGraphExec_t e = nullptr;
+    const int rc = check(hipGraphInstantiate(&e, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    (void)hipGraphDestroy(g);
+    if (rc) return -1;
+    *graph_exec = e;
+    return 0;
+}
+
+int snx_hip_graph_launch(void* graph_exec, void* stream) {
+    return check(hipGraphLaunch(reinterpret_cast<hipGraphExec_t>(graph_exec), S(stream)), "hipGraphLaunch");
+}
+
+int snx_hip_graph_destroy(void* graph_exec) {
+    return graph_exec ? check(hipGraphExecDestroy(reinterpret_cast<hipGraphExec_t>(graph_exec)),
+                              "hipGraphExecDestroy")
+                      : 0;
+}
+
 }  // extern "C"

@@ -353,7 +353,7 @@ int SNEPPX_dev_quantize_int8_channel_bf16(const uint16_t* in, int8_t* q, float* 
     REQUIRE(in && q && scales, "dev_quantize_int8_channel_bf16: NULL pointer");
     REQUIRE(rows && cols, "dev_quantize_int8_channel_bf16: empty matrix");
     snx_clear_error();
-    return snx_k_quant_int8_rows_bf16(in, q, scales, rows, cols, stream);
+    return snx_k_quant_rows_bf16_fast(in, q, scales, rows, cols, stream);
 }
 
 int SNEPPX_qlinear_w8a8_i8(const int8_t* A, const float* sA, const int8_t* W, const float* sW,
@@ -383,4 +383,48 @@ int SNEPPX_qlinear_w8a8_fp8(const uint8_t* A, const float* sA, const uint8_t* W,
     REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_fp8: A and W must be 16-byte aligned");
     snx_clear_error();
     return snx_k_fp8_gemm(A, W, sA, sW, out, bias, M, N, K, stream);
+}
+
+/* Workspace slot of the dynamically quantized activations (codes, then the
+ * per-token scales or the per-tensor scale record at a 256-byte boundary). */
+#define SLOT_W8A8_DYN 5
+
+int SNEPPX_qlinear_w8a8_i8_dyn(const uint16_t* A, const int8_t* W, const float* sW,
+                               const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                               SNEPPXStream stream) {
+    REQUIRE(A && W && sW && out, "qlinear_w8a8_i8_dyn: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w8a8_i8_dyn: empty shape");
+    REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_i8_dyn: A and W must be 16-byte aligned");
+    snx_clear_error();
+    const size_t qb = (M * K + 255) & ~(size_t)255;
+    char* ws = (char*)snx_workspace(qb + M * sizeof(float), SLOT_W8A8_DYN, stream);
+    if (!ws) return -1;
+    int8_t* aq = (int8_t*)ws;
+    float* sa = (float*)(ws + qb);
+    int rc = snx_k_quant_rows_bf16_fast(A, aq, sa, M, K, stream);
+    if (!rc) rc = snx_k_i8_gemm(aq, W, sa, sW, NULL, out, bias, M, N, K, stream);
+    return rc;
+}
+
+int SNEPPX_qlinear_w8a8_fp8_dyn(const uint16_t* A, const uint8_t* W, const float* sW,
+                                const float* bias, uint16_t* out, size_t M, size_t N, size_t K,
+                                SNEPPXStream stream) {
+    REQUIRE(A && W && sW && out, "qlinear_w8a8_fp8_dyn: NULL pointer");
+    REQUIRE(M && N && K, "qlinear_w8a8_fp8_dyn: empty shape");
+    REQUIRE(aligned16(A) && aligned16(W), "qlinear_w8a8_fp8_dyn: A and W must be 16-byte aligned");
+    snx_clear_error();
+    const size_t n = M * K, qb = (n + 255) & ~(size_t)255;
+    const int parts = snx_reduce_parts(n);
+    char* ws = (char*)snx_workspace(qb + ((size_t)parts * 2 + 64) * sizeof(float), SLOT_W8A8_DYN, stream);
+    if (!ws) return -1;
+    uint8_t* aq = (uint8_t*)ws;
+    float* part = (float*)(ws + qb);
+    float* rec = part + (size_t)parts * 2;
+    rec = (float*)(((uintptr_t)rec + 15u) & ~(uintptr_t)15u);
+    int rc = snx_k_absmax_bf16(A, n, part, parts, stream);
+    if (!rc) rc = snx_k_finalize_scale(part, parts, SNX_SCALE_FP8_240, NULL, rec, NULL, stream);
+    /* rec[0] = s_A, the per-tensor scale the GEMM's epilogue multiplies by */
+    if (!rc) rc = snx_k_fp8_encode_bf16(A, aq, n, rec, stream);
+    if (!rc) rc = snx_k_fp8_gemm(aq, W, rec, sW, out, bias, M, N, K, stream);
+    return rc;
 }

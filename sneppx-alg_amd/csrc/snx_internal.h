@@ -105,6 +105,14 @@ int snx_k_mx8_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const i
 int snx_k_quant_int8_modelzoo(const float* x, int8_t* q, size_t n, const float* rec,
                               void* stream);
 /* the same rule (roundf) on bf16 rows */
+/* per-token int8 of bf16 rows in one pass (row in registers; cols % 8 == 0,
+ * cols <= 8192, x 16-byte and q 8-byte aligned, else the two-pass kernel) */
+int snx_k_quant_rows_bf16_fast(const uint16_t* x, int8_t* q, float* scales, size_t rows, size_t cols,
+                               void* stream);
+/* partial max|x| of bf16 values / per-tensor scaled e4m3 codes of bf16 values
+ * (value / rec[0]) */
+int snx_k_absmax_bf16(const uint16_t* x, size_t n, float* part, int nparts, void* stream);
+int snx_k_fp8_encode_bf16(const uint16_t* x, uint8_t* c, size_t n, const float* rec, void* stream);
 int snx_k_quant_int8_rows_bf16(const uint16_t* x, int8_t* q, float* scales, size_t rows,
                                size_t cols, void* stream);
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* stream);

@@ -149,6 +149,12 @@ EXPORTS = {
     "snx_hip_stream_sync": (C.c_int, [_vp]),
     "snx_hip_device_info": (C.c_int, [C.c_char_p, _sz, C.POINTER(C.c_int), C.POINTER(C.c_int)]),
     "SNEPPX_qlinear_release_workspaces": (C.c_int, [_vp]),
+    "SNEPPX_qlinear_w8a8_i8_dyn": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "SNEPPX_qlinear_w8a8_fp8_dyn": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
+    "snx_hip_stream_begin_capture": (C.c_int, [_vp]),
+    "snx_hip_stream_end_capture": (C.c_int, [_vp, C.POINTER(_vp)]),
+    "snx_hip_graph_launch": (C.c_int, [_vp, _vp]),
+    "snx_hip_graph_destroy": (C.c_int, [_vp]),
     "snx_workspace_count": (C.c_long, []),
 }
 
@@ -429,6 +435,15 @@ class Library:
             _ptr(A), _ptr(sA), _ptr(W), _ptr(sW), _bias_ptr(bias, N, out), _ptr(out), M, N, K, self._stream(stream)),
             "qlinear_w8a8_i8")
 
+    def qlinear_w8a8_dyn(self, A, W, sW, out, fp8=False, stream=None, bias=None):
+        """C4 from bf16 activations: A quantized inside the call (int8 per
+        token, or fp8 per tensor), then the W8A8 GEMM."""
+        M, K = A.shape
+        N = W.shape[0]
+        name = "SNEPPX_qlinear_w8a8_fp8_dyn" if fp8 else "SNEPPX_qlinear_w8a8_i8_dyn"
+        self.check(self.fn[name](_ptr(A), _ptr(W), _ptr(sW), _bias_ptr(bias, N, out), _ptr(out), M, N, K,
+                                 self._stream(stream)), name[7:])
+
     def qlinear_i8_gemm_i32(self, A, W, Cm, stream=None):
         M, K = A.shape
         N = W.shape[0]
@@ -565,6 +580,25 @@ class Library:
 
     def record(self, ev, stream=None):
         self.check(self.fn["snx_hip_event_record"](ev, self._stream(stream)), "event_record")
+
+    def capture(self, fn, stream=None):
+        """A HIP graph of everything fn() issues on `stream` (an executable
+        graph handle; replay with graph_launch, free with graph_destroy)."""
+        st = self._stream(stream)
+        self.check(self.fn["snx_hip_stream_begin_capture"](st), "stream_begin_capture")
+        try:
+            fn()
+        finally:
+            g = C.c_void_p()
+            rc = self.fn["snx_hip_stream_end_capture"](st, C.byref(g))
+        self.check(rc, "stream_end_capture")
+        return g
+
+    def graph_launch(self, g, stream=None):
+        self.check(self.fn["snx_hip_graph_launch"](g, self._stream(stream)), "graph_launch")
+
+    def graph_destroy(self, g):
+        self.check(self.fn["snx_hip_graph_destroy"](g), "graph_destroy")
 
     def elapsed_ms(self, a, b):
         self.check(self.fn["snx_hip_event_sync"](b), "event_sync")

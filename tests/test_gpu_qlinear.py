@@ -635,10 +635,23 @@ def test_silu_mul_quant_int8_equals_quantizing_the_silu_output(lib, oracle, T, F
     np.testing.assert_array_equal(s.cpu().numpy().view(np.uint32), so.view(np.uint32))
 
 
-@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 4096), (2048, 4096), (3, 14336)])
+@pytest.mark.parametrize("rows,cols", [(1, 1), (7, 4096), (2048, 4096), (3, 14336), (5, 1000), (9, 2048),
+                                       (4, 6000), (3, 8192), (300, 136)])
 def test_dev_int8_channel_bf16_bit_exact(lib, oracle, rows, cols):
+    """Per-token int8 of bf16 rows (one-pass register kernel for cols % 8 == 0
+    up to 8192 in its 1 / 2 / 4-chunk forms, the two-pass kernel otherwise)
+    bit-exact vs the oracle, incl. NaN (ignored by the max, code -128), +-inf
+    (scale inf, codes 0 or NaN-clamped), an all-zero row (scale 1), bf16
+    denormals and exact .5 ties."""
     rng = np.random.default_rng(rows * cols)
-    xb = bf16_bits(rng.normal(0, 3, (rows, cols)).astype(np.float32))
+    x = rng.normal(0, 3, (rows, cols)).astype(np.float32)
+    if rows >= 3 and cols >= 8:
+        x[0, :4] = [np.nan, 1.0, -2.5, 127.0]
+        x[0, 4:8] = [0.5, 1.5, -0.5, 2.5]           # with max 127: exact ties
+        x[0, 8:] = np.clip(x[0, 8:], -126, 126)
+        x[1, :] = 0.0
+        x[2, :2] = [np.inf, -1e-39]
+    xb = bf16_bits(x)
     q = torch.empty((rows, cols), dtype=torch.int8, device=DEV)
     s = torch.empty(rows, device=DEV)
     lib.dev_quantize_int8_channel_bf16(to_dev(xb), q, s)
@@ -947,3 +960,41 @@ def test_decode_token_through_llama3_layer_linears(lib, oracle, tp):
     rc, gu = oracle.w4a16_linear(u16(o), qw, sc, qz, None, 2 * F, H, 128)
     g, u = gu[:, :F].astype(np.float64), gu[:, F:].astype(np.float64)
     assert rel_err(bf16_to_f32(u16(h)), g / (1.0 + np.exp(-g)) * u) <= TOL_BF16
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 14336, 4096), (300, 1000, 1024), (257, 448, 10016), (1, 256, 4096)])
+@pytest.mark.parametrize("fp8", [False, True])
+def test_w8a8_dyn_equals_quantize_then_gemm(lib, M, N, K, fp8):
+    """C4 from bf16 activations: the one-call form (A quantized inside) gives
+    the bits of quantizing A with the standalone entry point and calling the
+    GEMM (int8 per token; fp8 per tensor on A converted to fp32, exact)."""
+    print(f"[gpu] w8a8 dyn {'fp8' if fp8 else 'int8'} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(M + N + K)
+    A = torch.randn((M, K), device=DEV, generator=g).to(torch.bfloat16)
+    w = torch.randn((N, K), device=DEV, generator=g) * 0.02
+    bias = torch.randn(N, device=DEV, generator=g)
+    out1 = torch.empty((M, N), dtype=torch.bfloat16, device=DEV)
+    out2 = torch.empty_like(out1)
+    if fp8:
+        W = torch.empty((N, K), dtype=torch.uint8, device=DEV)
+        sW = torch.empty(1, device=DEV)
+        lib.dev_quantize_fp8_e4m3_scaled(w, W, sW)
+        lib.qlinear_w8a8_dyn(A.view(torch.int16), W, sW, out1, fp8=True, bias=bias)
+        Aq = torch.empty((M, K), dtype=torch.uint8, device=DEV)
+        sA = torch.empty(1, device=DEV)
+        lib.dev_quantize_fp8_e4m3_scaled(A.float(), Aq, sA)
+        lib.qlinear_w8a8_fp8(Aq, sA, W, sW, out2, bias=bias)
+    else:
+        W = torch.empty((N, K), dtype=torch.int8, device=DEV)
+        sW = torch.empty(N, device=DEV)
+        lib.dev_quantize_int8_channel(w, W, sW)
+        lib.qlinear_w8a8_dyn(A.view(torch.int16), W, sW, out1, bias=bias)
+        Aq = torch.empty((M, K), dtype=torch.int8, device=DEV)
+        sA = torch.empty(M, device=DEV)
+        lib.dev_quantize_int8_channel_bf16(A.view(torch.int16), Aq, sA)
+        lib.qlinear_w8a8_i8(Aq, sA, W, sW, out2, bias=bias)
+    torch.cuda.synchronize()
+    assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
+    ref = (A.float() @ w.T + bias).double()
+    err = (out1.double() - ref).abs().max() / ref.abs().max()
+    assert err < 0.05, err      # quantization error of both operands, not a parity bar
