@@ -55,7 +55,8 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0)
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
     p.add_argument("--graph", action="store_true", help="--only: time the decode lines as a HIP graph replay")
-    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-w4", "chain", "mx", "decode", "shard", "copy"],
+    p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-dyn", "gemm-w4", "chain", "mx", "decode",
+                                      "shard", "copy"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -865,6 +866,11 @@ def run_only(args, lib, timer, torch, N, K, group):
     if args.only == "gemv":
         r, _ = bench_w4a16(lib, timer, torch, args.m, N, K, group, args.copies, steps, args.warmup)
         print(f"gemv C2 M={args.m}: {r['ms_per_step'] * 1e3:.3f} us/launch, {r['gbs']:.0f} GB/s")
+    elif args.only == "gemm-dyn":
+        for fp8 in (False, True):
+            r = bench_w8a8_dyn(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fp8=fp8)
+            print(f"gemm-{'fp8' if fp8 else 'i8'} from bf16 A: {r['ms_per_step'] * 1e3:.1f} us/call, "
+                  f"{r['tops']:.0f} TOPS")
     elif args.only in ("gemm-i8", "gemm-fp8"):
         r = bench_w8a8(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fp8=args.only == "gemm-fp8")
         print(f"{args.only}: {r['ms_per_step'] * 1e3:.1f} us/launch, {r['tops']:.0f} TOPS")

@@ -997,4 +997,8 @@ def test_w8a8_dyn_equals_quantize_then_gemm(lib, M, N, K, fp8):
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16))
     ref = (A.float() @ w.T + bias).double()
     err = (out1.double() - ref).abs().max() / ref.abs().max()
-    assert err < 0.05, err      # quantization error of both operands, not a parity bar
+    # quantization error of both operands against the unquantized product,
+    # a sanity bound, not the parity bar (that is the bit equality above):
+    # the reference's e4m3 encoder truncates toward zero, so its errors share
+    # a sign and add up over K
+    assert err < (0.15 if fp8 else 0.05), err
