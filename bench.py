@@ -56,7 +56,7 @@ def parse():
     p.add_argument("--m", type=int, default=1, help="activation rows for --only gemv")
     p.add_argument("--graph", action="store_true", help="--only: time the decode lines as a HIP graph replay")
     p.add_argument("--only", choices=["gemv", "gemm-i8", "gemm-fp8", "gemm-dyn", "gemm-w4", "chain", "mx", "decode",
-                                      "shard", "copy"],
+                                      "shard", "copy", "fit"],
                    help="run one kernel family and exit (for rocprofv3 --pmc passes)")
     return p.parse_args()
 
@@ -860,12 +860,56 @@ def load_traffic(kernel):
     return int(rec["fetch_bytes"] + rec["write_bytes"])
 
 
+def intercept_fit(lib, timer, torch, steps, warmup, K=4096):
+    """Per-launch time of the M = 1 W4A16 GEMV (k_w4a16_gemv1) at six sizes
+    of N, and of a plain streaming read of the same bytes in the GEMV's
+    access shape (stream_read.hip: 16-byte nontemporal loads, 1 KB per wave
+    instruction, four per thread in flight, no arithmetic), each rotating
+    over enough copies to stream from HBM; least-squares fits
+    t = a + bytes / bw.  The intercept a is what a launch costs beyond its
+    bytes; the GEMV's minus the read's is what its own work adds.  The GEMV
+    is timed eagerly (launched from C) and as a graph replay, the read as a
+    graph replay."""
+    import numpy as np
+    bl = bench_loops()
+    bl.snxb_stream_read.restype = C.c_int
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    rows = []
+    for N in (2048, 4096, 8192, 11008, 16384, 28672):
+        nbytes = w4_bytes(1, N, K, K // 128)
+        cp = _copies_for(nbytes)
+        r, (ws, x, y, G) = bench_w4a16(lib, timer, torch, 1, N, K, 128, cp, steps, warmup, graph=False)
+        rg, _ = bench_w4a16(lib, timer, torch, 1, N, K, 128, cp, steps, warmup, graph=True)
+        del ws, x, y
+        rb = nbytes // 16 * 16
+        bufs = [torch.ones(rb // 4, dtype=torch.int32, device="cuda") for _ in range(cp)]
+        st = C.c_void_p(timer.stream)
+        calls = [lambda b=b: bl.snxb_stream_read(C.c_void_p(b.data_ptr()), C.c_size_t(rb),
+                                                 C.c_void_p(sink.data_ptr()), st) for b in bufs]
+        t_read, _, _ = timer.run(calls, steps, warmup, graph=True)
+        del bufs
+        rows.append({"N": N, "bytes": nbytes, "copies": cp, "gemv_us": round(r["ms_per_step"] * 1e3, 3),
+                     "gemv_graph_us": round(rg["ms_per_step"] * 1e3, 3),
+                     "read_graph_us": round(t_read / steps * 1e3, 3)})
+    b = np.array([r["bytes"] for r in rows], np.float64)
+    out = {"K": K, "steps": steps, "rows": rows}
+    for key in ("gemv_us", "gemv_graph_us", "read_graph_us"):
+        t = np.array([r[key] for r in rows], np.float64)
+        slope, icpt = np.polyfit(b, t, 1)
+        out[key.replace("_us", "_fit")] = {"intercept_us": round(float(icpt), 3),
+                                           "bw_tbs": round(float(1e-6 / slope), 3),
+                                           "max_resid_us": round(float(np.abs(t - (icpt + slope * b)).max()), 3)}
+    return out
+
+
 def run_only(args, lib, timer, torch, N, K, group):
     """One kernel family, for profiler passes (prints one line, no JSON)."""
     steps = args.steps
     if args.only == "gemv":
         r, _ = bench_w4a16(lib, timer, torch, args.m, N, K, group, args.copies, steps, args.warmup)
         print(f"gemv C2 M={args.m}: {r['ms_per_step'] * 1e3:.3f} us/launch, {r['gbs']:.0f} GB/s")
+    elif args.only == "fit":
+        print(json.dumps(intercept_fit(lib, timer, torch, steps, args.warmup)), flush=True)
     elif args.only == "gemm-dyn":
         for fp8 in (False, True):
             r = bench_w8a8_dyn(lib, timer, torch, 2048, 14336, 4096, steps, args.warmup, fp8=fp8)
