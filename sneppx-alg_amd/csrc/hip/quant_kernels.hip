@@ -298,10 +298,19 @@ __global__ void __launch_bounds__(256) k_absmax_bf16_v8(const uint16_t* __restri
     if (threadIdx.x == 0) part[blockIdx.x] = m;
 }
 
+// The scale comes from the partial maxima: every block reduces them (nparts
+// floats from L2) to s = max/240 (1 below FLT_MIN), the rule of k_finalize's
+// SNX_SCALE_FP8_240, and block 0 writes it to *scale_out for the GEMM.
 __global__ void __launch_bounds__(256) k_fp8_encode_bf16_v8(const uint16_t* __restrict__ x,
                                                             uint8_t* __restrict__ c, size_t n8,
-                                                            const float* __restrict__ rec) {
-    const float s = rec[0];
+                                                            const float* __restrict__ part, int nparts,
+                                                            float* __restrict__ scale_out) {
+    __shared__ float sh[16];
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = nanless_max(m, part[i]);
+    m = block_reduce(m, nanless_max, sh);
+    const float s = m < FLT_MIN ? 1.0f : m / 240.0f;
+    if (blockIdx.x == 0 && threadIdx.x == 0) scale_out[0] = s;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n8; i += (size_t)gridDim.x * blockDim.x) {
         const uint4 v = reinterpret_cast<const uint4*>(x)[i];
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
@@ -838,12 +847,15 @@ int snx_k_absmax_bf16(const uint16_t* x, size_t n, float* part, int nparts, void
     return snx_launch_check("k_absmax_bf16");
 }
 
+int snx_k_fp8_encode_bf16_pt(const uint16_t* x, uint8_t* c, size_t n, const float* part, int nparts,
+                             float* scale_out, void* st) {
+    k_fp8_encode_bf16_v8<<<grid_for(n / 8, kBlock * 2), kBlock, 0, S(st)>>>(x, c, n / 8, part, nparts, scale_out);
+    return snx_launch_check("k_fp8_encode_bf16_v8");
+}
+
 int snx_k_fp8_encode_bf16(const uint16_t* x, uint8_t* c, size_t n, const float* rec, void* st) {
     if (n == 0) return 0;
-    if (n % 8 == 0 && ((uintptr_t)x & 15u) == 0 && ((uintptr_t)c & 7u) == 0)
-        k_fp8_encode_bf16_v8<<<grid_for(n / 8, kBlock * 2), kBlock, 0, S(st)>>>(x, c, n / 8, rec);
-    else
-        k_fp8_encode<0, uint16_t><<<grid_for(n, kBlock * 4), kBlock, 0, S(st)>>>(x, c, n, rec);
+    k_fp8_encode<0, uint16_t><<<grid_for(n, kBlock * 4), kBlock, 0, S(st)>>>(x, c, n, rec);
     return snx_launch_check("k_fp8_encode_bf16");
 }
 

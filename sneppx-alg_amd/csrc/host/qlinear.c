@@ -422,9 +422,15 @@ int SNEPPX_qlinear_w8a8_fp8_dyn(const uint16_t* A, const uint8_t* W, const float
     float* rec = part + (size_t)parts * 2;
     rec = (float*)(((uintptr_t)rec + 15u) & ~(uintptr_t)15u);
     int rc = snx_k_absmax_bf16(A, n, part, parts, stream);
-    if (!rc) rc = snx_k_finalize_scale(part, parts, SNX_SCALE_FP8_240, NULL, rec, NULL, stream);
-    /* rec[0] = s_A, the per-tensor scale the GEMM's epilogue multiplies by */
-    if (!rc) rc = snx_k_fp8_encode_bf16(A, aq, n, rec, stream);
+    /* rec[0] = s_A, the per-tensor scale the GEMM's epilogue multiplies by:
+     * the encode kernel reduces the partials itself when it can take the
+     * vector path, else a one-block finalize does */
+    if (!rc && n % 8 == 0 && ((uintptr_t)aq & 7u) == 0) {
+        rc = snx_k_fp8_encode_bf16_pt(A, aq, n, part, parts, rec, stream);
+    } else if (!rc) {
+        rc = snx_k_finalize_scale(part, parts, SNX_SCALE_FP8_240, NULL, rec, NULL, stream);
+        if (!rc) rc = snx_k_fp8_encode_bf16(A, aq, n, rec, stream);
+    }
     if (!rc) rc = snx_k_fp8_gemm(aq, W, rec, sW, out, bias, M, N, K, stream);
     return rc;
 }

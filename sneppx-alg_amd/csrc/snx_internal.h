@@ -113,6 +113,11 @@ int snx_k_quant_rows_bf16_fast(const uint16_t* x, int8_t* q, float* scales, size
  * (value / rec[0]) */
 int snx_k_absmax_bf16(const uint16_t* x, size_t n, float* part, int nparts, void* stream);
 int snx_k_fp8_encode_bf16(const uint16_t* x, uint8_t* c, size_t n, const float* rec, void* stream);
+/* the same from the nparts partial maxima of snx_k_absmax_bf16, the scale
+ * (max/240) computed in every block and written to *scale_out; n % 8 == 0,
+ * x 16-byte and c 8-byte aligned */
+int snx_k_fp8_encode_bf16_pt(const uint16_t* x, uint8_t* c, size_t n, const float* part, int nparts,
+                             float* scale_out, void* stream);
 int snx_k_quant_int8_rows_bf16(const uint16_t* x, int8_t* q, float* scales, size_t rows,
                                size_t cols, void* stream);
 int snx_k_fake_quant(const float* x, float* y, size_t n, float scale, int bits, void* stream);
