@@ -116,7 +116,8 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // output column, so waves 0-3 hold gate values and waves 4-7 the matching up
 // values; the epilogue pairs them through LDS.
 // SPLIT > 1 (too few tiles to fill the CUs, such as the QKV projection of one
-// GPU's tensor-parallel shard): workgroup unit v covers tile v % ntiles and
+// GPU's tensor-parallel shard, or the tiles past the last full round of
+// CUs): workgroup unit v covers tile tile0 + v % ntiles and
 // the K steps of span v / ntiles (K / SPLIT columns).  Each wave stores its
 // span's fp32 results to its slot of `part` (system-coherent policy, so no
 // L2 keeps a copy another XCD cannot see), waits until they are written and
@@ -133,7 +134,8 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                                                     void* __restrict__ y,
                                                     const float* __restrict__ bias, int M, int N,
                                                     int K, int G, int gshift, int Mp, int tiles_m,
-                                                    u32x4* __restrict__ part, uint32_t* __restrict__ cnt) {
+                                                    u32x4* __restrict__ part, uint32_t* __restrict__ cnt,
+                                                    int tile0) {
     static_assert(SPLIT == 1 || !SWIGLU, "the SwiGLU epilogue takes whole-K tiles");
     // WN waves along N, 8 / WN along M: each wave owns RW rows x CW columns,
     // FM x FN blocks of 32 x 32; the result sits in FM / 2 x FN pairs of
@@ -150,9 +152,11 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     // XCD-aware order: consecutive units of one M-row of tiles share an XCD
     const int b = blockIdx.x, nb = gridDim.x;
     const int unit = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
+    // this launch covers tiles tile0 .. tile0 + ntiles - 1 (the span
+    // partials and counters are indexed by the launch's own tile number)
     const int ntiles = nb / SPLIT;
     const int tile = SPLIT == 1 ? unit : unit % ntiles, span = SPLIT == 1 ? 0 : unit / ntiles;
-    const int tm = tile % tiles_m, tn = tile / tiles_m;
+    const int tm = (tile0 + tile) % tiles_m, tn = (tile0 + tile) / tiles_m;
     const int m0 = tm * GBM, n0 = tn * (SWIGLU ? GBN / 2 : GBN);
     // weight row of tile column c (clamped into the matrix)
     auto wcol = [&](int c) -> int {
@@ -511,12 +515,16 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     }
 }
 
+// Launches tiles [tile0, tile0 + count) of the tile grid (all of it when
+// count < 0) in SPLIT K spans.
 template <bool ZEROS, bool YF32, int WN, bool SWIGLU, int SPLIT>
 int launch_w4_gemm_s(const uint16_t* xp, const float* xs, const uint32_t* qw,
                      const uint16_t* scales, const uint32_t* qz, void* y, const float* bias, int M,
-                     int N, int K, int group, int Mp, void* part, uint32_t* cnt, hipStream_t st) {
+                     int N, int K, int group, int Mp, void* part, uint32_t* cnt, hipStream_t st,
+                     int tile0 = 0, int count = -1) {
     const int tn_cols = SWIGLU ? GBN / 2 : GBN;
     const int tiles_m = (M + GBM - 1) / GBM, tiles_n = (N + tn_cols - 1) / tn_cols;
+    const int ntiles = count < 0 ? tiles_m * tiles_n : count;
     const size_t lds = (size_t)GSTAGES * GRING;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
     const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU, SPLIT>);
@@ -525,9 +533,9 @@ int launch_w4_gemm_s(const uint16_t* xp, const float* xs, const uint32_t* qw,
         return -1;
     }
     const int gshift = __builtin_ctz((unsigned)group);
-    k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU, SPLIT><<<tiles_m * tiles_n * SPLIT, 512, lds, st>>>(
+    k_w4a16_gemm<ZEROS, YF32, WN, SWIGLU, SPLIT><<<ntiles * SPLIT, 512, lds, st>>>(
         xp, xs, qw, scales, qz, y, bias, M, N, K, K / group, gshift, Mp, tiles_m,
-        static_cast<u32x4*>(part), cnt);
+        static_cast<u32x4*>(part), cnt, tile0);
     return snx_launch_check("k_w4a16_gemm");
 }
 
@@ -539,9 +547,21 @@ int launch_w4_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
         if (split == 4)
             return launch_w4_gemm_s<ZEROS, YF32, WN, false, 4>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
                                                                part, cnt, st);
-        if (split == 2)
+        if (split == 2) {
+            const int ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN), ncu = snx::cu_count();
+            if (ntiles > ncu) {
+                // the full rounds whole-K, the remaining tiles (at most half a
+                // round) in two spans on twice as many workgroups
+                const int full = ntiles - ntiles % ncu;
+                const int rc = launch_w4_gemm_s<ZEROS, YF32, WN, false, 1>(xp, xs, qw, scales, qz, y, bias, M, N, K,
+                                                                           group, Mp, nullptr, nullptr, st, 0, full);
+                if (rc) return rc;
+                return launch_w4_gemm_s<ZEROS, YF32, WN, false, 2>(xp, xs, qw, scales, qz, y, bias, M, N, K, group,
+                                                                   Mp, part, cnt, st, full, ntiles - full);
+            }
             return launch_w4_gemm_s<ZEROS, YF32, WN, false, 2>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
                                                                part, cnt, st);
+        }
     }
     return launch_w4_gemm_s<ZEROS, YF32, WN, SWIGLU, 1>(xp, xs, qw, scales, qz, y, bias, M, N, K, group, Mp,
                                                          nullptr, nullptr, st);
@@ -699,19 +719,28 @@ int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t
 
 // K spans of the prefill GEMM for M x N x K (no SwiGLU step): 4 or 2 when
 // the tiles fill at most a quarter or a half of the CUs and each span keeps
-// at least two 128-column steps, else 1.
+// at least two 128-column steps; 2 as well when the tiles exceed a round of
+// the CUs by at most half a round (the launcher then runs the full rounds
+// whole-K and only the remaining tiles in two spans: the QKV projection's
+// 360 tiles on 256 CUs); else 1.
 int snx_w4a16_gemm_splits(size_t M, size_t N, size_t K) {
     const size_t ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
     const size_t ncu = (size_t)snx::cu_count(), nk = K / GBK;
     if (ntiles * 4 <= ncu && nk % 4 == 0 && nk >= 8) return 4;
     if (ntiles * 2 <= ncu && nk % 2 == 0 && nk >= 4) return 2;
+    const size_t rem = ntiles % ncu;
+    if (ntiles > ncu && rem > 0 && rem * 2 <= ncu && nk % 2 == 0 && nk >= 4) return 2;
     return 1;
 }
 
 // Bytes of the span partials (`part`) and arrival counters (`cnt`) of a
-// `splits`-span call: a 16 KB slot per (unit, wave), a counter per (tile, wave).
+// `splits`-span call: a 16 KB slot per (unit, wave) of the tiles that take
+// spans (past a full round of CUs only the remaining ones), a counter per
+// (tile, wave).
 size_t snx_w4a16_gemm_part_bytes(size_t M, size_t N, int splits) {
-    const size_t ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    size_t ntiles = ((M + GBM - 1) / GBM) * ((N + GBN - 1) / GBN);
+    const size_t ncu = (size_t)snx::cu_count();
+    if (ntiles > ncu) ntiles %= ncu;
     return ntiles * (size_t)splits * 8 * (2 * 8 * 64 * 16);
 }
 size_t snx_w4a16_gemm_cnt_bytes(size_t M, size_t N) {

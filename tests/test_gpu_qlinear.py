@@ -468,11 +468,14 @@ def test_w4a16_gemm_output_rows_staged_or_not(lib, oracle, N, out, yoff):
         assert float(buf[:yoff].abs().max()) == 0.0       # nothing written before the output
 
 
-@pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (600, 4096, 14336), (1849, 768, 4096)])
+@pytest.mark.parametrize("M,N,K", [(2192, 6144, 4096), (1849, 6144, 4096), (600, 4096, 14336),
+                                   (1849, 768, 4096)])
 def test_w4a16_gemm_llama_shapes_sampled_rows(lib, oracle, M, N, K):
-    """Full-size QKV (T=2192) and down-projection shapes, and the QKV
-    projection of one GPU's tensor-parallel shard (N = 6144 / 8: 45 tiles,
-    K in 4 spans; the down shape at M = 600 runs 2): weights quantized on
+    """Full-size QKV (T=2192; and T=1849, whose 360 tiles exceed a round of
+    256 CUs by 104: the full round whole-K, the 104 in two K spans) and
+    down-projection shapes, and the QKV projection of one GPU's
+    tensor-parallel shard (N = 6144 / 8: 45 tiles, K in 4 spans; the down
+    shape at M = 600 runs 2): weights quantized on
     the GPU (bit-exact quantizer), every output row of a sample checked
     against the oracle, including the last, partial M tile; a second call
     gives bit-identical output (the span sums' order does not depend on
