@@ -80,6 +80,7 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
 
 // ----------------------------------------------------------------- the GEMM
 constexpr int W4_WN = 8;   // waves along N (8 / W4_WN along M)
+constexpr int W4_GROUP_M = 8;   // rows of tiles per band of the tile order
 // LDS ring of three stages (one K step of 128 columns each):
 //   A   128 rows x 256 B  bf16 activations, chunk c of row r at c ^ (r & 15)
 //   B   256 rows x 64 B   packed weights,   chunk c of row r at c ^ bsw(r)
@@ -149,14 +150,26 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
     const int wm = wave / WN, wn = wave % WN;
     const int r32 = lane & 31, h = lane >> 5;
 
-    // XCD-aware order: consecutive units of one M-row of tiles share an XCD
+    // XCD-aware order: consecutive units share an XCD
     const int b = blockIdx.x, nb = gridDim.x;
     const int unit = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
     // this launch covers tiles tile0 .. tile0 + ntiles - 1 (the span
     // partials and counters are indexed by the launch's own tile number)
     const int ntiles = nb / SPLIT;
     const int tile = SPLIT == 1 ? unit : unit % ntiles, span = SPLIT == 1 ? 0 : unit / ntiles;
-    const int tm = (tile0 + tile) % tiles_m, tn = (tile0 + tile) / tiles_m;
+    // tile t -> (tm, tn) in bands of W4_GROUP_M rows of tiles, M fastest
+    // within a band: the ~32 tiles an XCD runs at once span 8 activation row
+    // blocks and ~4 weight column blocks, so every K step's slices are
+    // shared by several of them in the XCD's L2 (row-major order over all
+    // 15 row blocks of T = 1849 shared each activation slice by only ~2)
+    int tm, tn;
+    {
+        const int tiles_n = (N + (SWIGLU ? GBN / 2 : GBN) - 1) / (SWIGLU ? GBN / 2 : GBN);
+        const int t = tile0 + tile, band = W4_GROUP_M * tiles_n, g = t / band, r = t - g * band;
+        const int gm = tiles_m - g * W4_GROUP_M < W4_GROUP_M ? tiles_m - g * W4_GROUP_M : W4_GROUP_M;
+        tm = g * W4_GROUP_M + r % gm;
+        tn = r / gm;
+    }
     const int m0 = tm * GBM, n0 = tn * (SWIGLU ? GBN / 2 : GBN);
     // weight row of tile column c (clamped into the matrix)
     auto wcol = [&](int c) -> int {
