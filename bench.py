@@ -496,7 +496,9 @@ def bench_chain(lib, timer, torch, steps, warmup, tp=1):
     """C5: one Llama-3-8B decoder layer's linears in W4A16 g128 (AWQ-style,
     random init): QKV 4096->6144, O 4096->4096, gate/up 4096->2x14336 with
     SiLU(gate)*up in the GEMM's epilogue, down 14336->4096, on T packed
-    tokens.  The O input is a
+    tokens; gate/up and down run as one MLP call (SNEPPX_qlinear_w4a16_mlp:
+    the SwiGLU rows are written as the down projection's prepared input).
+    The O input is a
     synthetic bf16 tensor (attention is not part of this path); the gate/up
     input is the O output.  tp > 1: one GPU's shard of a tp-way
     tensor-parallel layer (QKV, gate/up N / tp; O, down K / tp; the
@@ -533,11 +535,13 @@ def bench_chain(lib, timer, torch, steps, warmup, tp=1):
         qw, sc, qz, G = ws["gate_up"]
         lib.qlinear_w4a16_swiglu(inp, qw, sc, qz, out, 128, stream=st)
 
+    def mlp(inp, out):
+        lib.qlinear_w4a16_mlp(inp, ws["gate_up"][:3], ws["down"][:3], out, 128, stream=st)
+
     def layer():
         lin("qkv", x, y_qkv)
         lin("o", attn, y_o)
-        gate_up_swiglu(y_o, act)           # gate/up GEMM with SiLU(gate) * up in its epilogue
-        lin("down", act, y_d)
+        mlp(y_o, y_d)                      # gate/up + SiLU(gate) * up -> down
 
     total, _, _ = timer.run([layer], steps, warmup)
     per = {}
@@ -547,6 +551,10 @@ def bench_chain(lib, timer, torch, steps, warmup, tp=1):
         t, _, _ = timer.run([fn], steps, 2)
         N, K = shapes[name.split("+")[0]]
         per[name] = {"us": round(t / steps * 1e3, 1), "tflops": round(2 * T * N * K / (t / steps) / 1e9, 1)}
+    t, _, _ = timer.run([lambda: mlp(y_o, y_d)], steps, 2)
+    fl = 2 * T * (shapes["gate_up"][0] * shapes["gate_up"][1] + shapes["down"][0] * shapes["down"][1])
+    per["mlp (gate_up+swiglu -> down, one call)"] = {"us": round(t / steps * 1e3, 1),
+                                                     "tflops": round(fl / (t / steps) / 1e9, 1)}
     # the unfused form for comparison: the [T][2F] projection in bf16, then the SwiGLU pass
     t, _, _ = timer.run([lambda: (lin("gate_up", y_o, y_gu), lib.qlinear_silu_mul(y_gu, act, stream=st))],
                         steps, 2)

@@ -187,6 +187,25 @@ int SNEPPX_qlinear_w4a16_swiglu(const uint16_t* x, const uint32_t* qweight,
                                 uint16_t* out, size_t M, size_t F, size_t K, int group,
                                 SNEPPXStream stream);
 
+/* A SwiGLU MLP block in W4A16 (no single reference counterpart: it is
+ * SNEPPX_qlinear_w4a16_swiglu followed by SNEPPX_qlinear_w4a16 on its
+ * output, the SwiGLU rule of gated_activations.c:33-52 between the two
+ * projections): y[m][n] = down(silu(gate(x)) * up(x)).
+ * x bf16 [M][H]; gate/up weights as for SNEPPX_qlinear_w4a16_swiglu
+ * (stacked [2F][H], gu_bias fp32 [2F] or NULL); down weights as for
+ * SNEPPX_qlinear_w4a16 with K = F (dn_bias fp32 [N] or NULL); y [M][N] in
+ * y_dtype (bf16 or fp32); one group size for both projections.  For
+ * prefill row counts the gate/up GEMM writes its SwiGLU rows straight into
+ * the down GEMM's prepared input (F % 128 == 0), which saves the down
+ * projection's activation pass; the results are bit-identical to the two
+ * calls above (which is what other shapes run).  Scratch: the calling
+ * thread's workspaces on `stream`. */
+int SNEPPX_qlinear_w4a16_mlp(const uint16_t* x, const uint32_t* gu_qweight, const uint16_t* gu_scales,
+                             const uint32_t* gu_qzeros, const float* gu_bias, const uint32_t* dn_qweight,
+                             const uint16_t* dn_scales, const uint32_t* dn_qzeros, const float* dn_bias,
+                             void* y, SNEPPXDtype y_dtype, size_t M, size_t H, size_t F, size_t N,
+                             int group, SNEPPXStream stream);
+
 /* SNEPPX_qlinear_silu_mul fused with the per-token int8 quantizer the W8A8
  * down projection needs (no reference counterpart; the rule is
  * SNEPPX_quantize_int8_channel, quantize_int8.c:157-177, applied to the bf16

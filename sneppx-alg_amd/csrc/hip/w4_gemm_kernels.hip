@@ -116,6 +116,13 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // column n0 + c, column c >= 128 the up column F + n0 + c - 128 of the same
 // output column, so waves 0-3 hold gate values and waves 4-7 the matching up
 // values; the epilogue pairs them through LDS.
+// PREP (SwiGLU only): the output is written as the next projection's
+// prepared input instead of plain rows (a SwiGLU MLP's down projection reads
+// exactly silu(gate) * up): tile column block tn is that projection's
+// 128-column step tn, so y takes the bf16 values in the prep pass's slot
+// order and `part`, read as float [F / 128][Mp], the step sums, summed in
+// the prep pass's order (bit-identical to running the prep pass on the plain
+// rows).
 // SPLIT > 1 (too few tiles to fill the CUs, such as the QKV projection of one
 // GPU's tensor-parallel shard, or the tiles past the last full round of
 // CUs): workgroup unit v covers tile tile0 + v % ntiles and
@@ -126,7 +133,7 @@ __device__ __forceinline__ int bsw(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 // (tile, wave) adds the slots in span order (the same fp32 sums whichever
 // wave is last), returns the counter to 0 and writes the output.  No wave
 // waits for another.
-template <bool ZEROS, bool YF32, int WN, bool SWIGLU, int SPLIT = 1>
+template <bool ZEROS, bool YF32, int WN, bool SWIGLU, int SPLIT = 1, bool PREP = false>
 __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__ xp,
                                                     const float* __restrict__ xs,
                                                     const uint32_t* __restrict__ qw,
@@ -138,6 +145,7 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                                                     u32x4* __restrict__ part, uint32_t* __restrict__ cnt,
                                                     int tile0) {
     static_assert(SPLIT == 1 || !SWIGLU, "the SwiGLU epilogue takes whole-K tiles");
+    static_assert(!PREP || (SWIGLU && !YF32), "the prepared output is the SwiGLU form's bf16 rows");
     // WN waves along N, 8 / WN along M: each wave owns RW rows x CW columns,
     // FM x FN blocks of 32 x 32; the result sits in FM / 2 x FN pairs of
     // blocks stacked along M (the 2-block f32 MFMA's output)
@@ -486,6 +494,42 @@ __global__ void __launch_bounds__(512) k_w4a16_gemm(const uint16_t* __restrict__
                     ex[c * XS + 32 * (2 * i + u) + 8 * (v >> 2) + 4 * h + (v & 3)] = yq[i][0][16 * u + v] + bv;
         __builtin_amdgcn_s_waitcnt(0xc07f);
         __builtin_amdgcn_s_barrier();
+        if constexpr (PREP) {
+            // wave w: output rows 16 w .. 16 w + 15, four per pass; lane l
+            // takes the 8 columns of chunk j = l % 16 of row 16 w + 4 p + l / 16.
+            // The 16 lanes of a row are the 16 threads of one step in the prep
+            // pass (same chunk sums, same xor butterfly), and chunk j goes to
+            // slot chunk 2 (j % 8) + j / 8 with its values in the order
+            // {0,4,1,5,2,6,3,7}.  Host: F % 128 == 0, rows 16-byte aligned.
+            const int j = lane & 15, jout = 2 * (j & 7) + (j >> 3);
+            uint16_t* xo = static_cast<uint16_t*>(y);
+            float* so = reinterpret_cast<float*>(part);
+            const int step = n0 / (GBN / 2);
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                const int row = 16 * wave + 4 * p + (lane >> 4), m = m0 + row;
+                uint32_t a[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const int oc = 8 * j + e;
+                    a[e] = bf16_out(silu_mul_fast(ex[oc * XS + row], ex[(oc + GBN / 2) * XS + row]));
+                }
+                float sum = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    sum += __builtin_bit_cast(float, a[2 * e] << 16) + __builtin_bit_cast(float, a[2 * e + 1] << 16);
+                sum += __shfl_xor(sum, 8);
+                sum += __shfl_xor(sum, 4);
+                sum += __shfl_xor(sum, 2);
+                sum += __shfl_xor(sum, 1);
+                if (m < M) {
+                    const u32x4 pk = {a[0] | a[4] << 16, a[1] | a[5] << 16, a[2] | a[6] << 16, a[3] | a[7] << 16};
+                    *reinterpret_cast<u32x4*>(xo + (size_t)m * N + (size_t)step * (GBN / 2) + jout * 8) = pk;
+                    if (j == 0) so[(size_t)step * Mp + m] = sum;
+                }
+            }
+            return;
+        }
         // wave w: output rows 16 w .. 16 w + 15, two columns per lane
         const int oc = 2 * (lane & 63);                         // output column pair 0..126
         const int n = n0 + oc;
@@ -775,6 +819,32 @@ int snx_k_w4a16_gemm(const uint16_t* xp, const float* xs, const uint32_t* qw,
     }
     if (y_f32) return launch_w4_gemm<false, true, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
     return launch_w4_gemm<false, false, W4_WN, false>(xp, xs, qw, scales, qzeros, y, bias, m, n, k, group, mp, splits, part, cnt, S(st));
+}
+
+int snx_k_w4a16_gemm_swiglu_prep(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                                 const uint16_t* scales, const uint32_t* qzeros, uint16_t* out_xp,
+                                 float* out_xs, const float* bias, size_t M, size_t F, size_t K, int group,
+                                 size_t Mp, void* st) {
+    const int m = (int)M, f = (int)F, k = (int)K, mp = (int)Mp;
+    const int tiles_m = (m + GBM - 1) / GBM, tiles_n = (f + GBN / 2 - 1) / (GBN / 2);
+    const size_t lds = (size_t)GSTAGES * GRING;
+    const int gshift = __builtin_ctz((unsigned)group);
+    static std::atomic<uint64_t> lds_done[2];   // > 64 KB of LDS per workgroup, per device
+#define SNX_GP(Z)                                                                                        \
+    do {                                                                                                 \
+        const void* kfn = reinterpret_cast<const void*>(&k_w4a16_gemm<Z, false, W4_WN, true, 1, true>); \
+        if (snx::lds_optin(kfn, (int)lds, lds_done[Z ? 1 : 0]) != hipSuccess) {                         \
+            snx_set_error("w4a16 gemm: cannot reserve %zu bytes of LDS", lds);                          \
+            return -1;                                                                                   \
+        }                                                                                                \
+        k_w4a16_gemm<Z, false, W4_WN, true, 1, true><<<tiles_m * tiles_n, 512, lds, S(st)>>>(           \
+            xp, xs, qw, scales, qzeros, out_xp, bias, m, f, k, k / group, gshift, mp, tiles_m,           \
+            reinterpret_cast<u32x4*>(out_xs), nullptr, 0);                                               \
+    } while (0)
+    if (qzeros) SNX_GP(true);
+    else SNX_GP(false);
+#undef SNX_GP
+    return snx_launch_check("k_w4a16_gemm");
 }
 
 int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t* qw,

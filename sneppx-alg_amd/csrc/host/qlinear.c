@@ -327,6 +327,65 @@ int SNEPPX_qlinear_w4a16_swiglu(const uint16_t* x, const uint32_t* qweight,
     return rc;
 }
 
+/* workspace slot of the MLP's SwiGLU rows (prepared or plain) */
+#define SLOT_MLP_ACT 6
+
+int SNEPPX_qlinear_w4a16_mlp(const uint16_t* x, const uint32_t* gu_qweight, const uint16_t* gu_scales,
+                             const uint32_t* gu_qzeros, const float* gu_bias, const uint32_t* dn_qweight,
+                             const uint16_t* dn_scales, const uint32_t* dn_qzeros, const float* dn_bias,
+                             void* y, SNEPPXDtype y_dtype, size_t M, size_t H, size_t F, size_t N,
+                             int group, SNEPPXStream stream) {
+    REQUIRE(x && gu_qweight && gu_scales && dn_qweight && dn_scales && y, "qlinear_w4a16_mlp: NULL pointer");
+    REQUIRE(M && H && F && N, "qlinear_w4a16_mlp: empty shape");
+    REQUIRE(F % 8 == 0 && H % 8 == 0, "qlinear_w4a16_mlp: F=%zu and H=%zu must be multiples of 8", F, H);
+    REQUIRE(group > 0 && H % (size_t)group == 0 && F % (size_t)group == 0,
+            "qlinear_w4a16_mlp: group %d must divide H=%zu and F=%zu", group, H, F);
+    REQUIRE(y_dtype == SNEPPX_BFLOAT16 || y_dtype == SNEPPX_FLOAT32,
+            "qlinear_w4a16_mlp: y_dtype must be SNEPPX_BFLOAT16 or SNEPPX_FLOAT32");
+    snx_clear_error();
+    const int aligned = aligned16(x) && aligned16(gu_qweight) && aligned16(dn_qweight) &&
+                        ((uintptr_t)gu_scales & 3u) == 0 && ((uintptr_t)gu_qzeros & 3u) == 0 &&
+                        ((uintptr_t)dn_scales & 3u) == 0 && ((uintptr_t)dn_qzeros & 3u) == 0;
+    if (M >= SNX_W4_GEMM_MIN_M && aligned && F % 128 == 0 && snx_w4a16_gemm_ok(M, 2 * F, H, group) &&
+        snx_w4a16_gemm_ok(M, N, F, group)) {
+        /* x prepared once; the gate/up GEMM's SwiGLU epilogue writes the down
+         * GEMM's prepared input (slot order + step sums) */
+        const size_t Mp = snx_w4_prep_rows(M);
+        const size_t xp_bytes = (M * H * sizeof(uint16_t) + 255) & ~(size_t)255;
+        char* ws = (char*)snx_workspace(xp_bytes + (H / 128) * Mp * sizeof(float), 1, stream);
+        const size_t ap_bytes = (M * F * sizeof(uint16_t) + 255) & ~(size_t)255;
+        char* wa = (char*)snx_workspace(ap_bytes + (F / 128) * Mp * sizeof(float), SLOT_MLP_ACT, stream);
+        if (!ws || !wa) return -1;
+        uint16_t* xp = (uint16_t*)ws;
+        float* xs = (float*)(ws + xp_bytes);
+        uint16_t* ap = (uint16_t*)wa;
+        float* as = (float*)(wa + ap_bytes);
+        const int splits = snx_w4a16_gemm_splits(M, N, F);
+        void* part = NULL;
+        uint32_t* cnt = NULL;
+        if (splits > 1) {
+            part = snx_workspace(snx_w4a16_gemm_part_bytes(M, N, splits), 3, stream);
+            cnt = (uint32_t*)snx_workspace_zeroed(snx_w4a16_gemm_cnt_bytes(M, N), 4, stream);
+            if (!part || !cnt) return -1;
+        }
+        int rc = snx_k_w4_prep_x(x, xp, xs, M, H, Mp, stream);
+        if (!rc) rc = snx_k_w4a16_gemm_swiglu_prep(xp, xs, gu_qweight, gu_scales, gu_qzeros, ap, as, gu_bias,
+                                                   M, F, H, group, Mp, stream);
+        if (!rc) rc = snx_k_w4a16_gemm(ap, as, dn_qweight, dn_scales, dn_qzeros, y, dn_bias,
+                                       y_dtype == SNEPPX_FLOAT32, M, N, F, group, Mp, splits, part, cnt,
+                                       stream);
+        return rc;
+    }
+    /* other shapes: the two linears, the SwiGLU rows in a workspace */
+    uint16_t* act = (uint16_t*)snx_workspace(M * F * sizeof(uint16_t), SLOT_MLP_ACT, stream);
+    if (!act) return -1;
+    int rc = SNEPPX_qlinear_w4a16_swiglu(x, gu_qweight, gu_scales, gu_qzeros, gu_bias, act, M, F, H, group,
+                                         stream);
+    if (!rc) rc = SNEPPX_qlinear_w4a16(act, dn_qweight, dn_scales, dn_qzeros, NULL, 0, dn_bias, y, y_dtype,
+                                       M, N, F, group, stream);
+    return rc;
+}
+
 int SNEPPX_qlinear_silu_mul(const uint16_t* gate_up, uint16_t* out, size_t T, size_t F,
                             SNEPPXStream stream) {
     REQUIRE(gate_up && out, "qlinear_silu_mul: NULL pointer");

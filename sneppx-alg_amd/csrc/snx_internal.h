@@ -215,6 +215,13 @@ int snx_k_w4a16_gemm_swiglu(const uint16_t* xp, const float* xs, const uint32_t*
                             const uint16_t* scales, const uint32_t* qzeros, uint16_t* out,
                             const float* bias, size_t M, size_t F, size_t K, int group, size_t Mp,
                             void* stream);
+/* the same GEMM writing its SwiGLU rows as the down projection's prepared
+ * input: out_xp [M][F] in the prep pass's slot order, out_xs [F / 128][Mp]
+ * step sums (F % 128 == 0) */
+int snx_k_w4a16_gemm_swiglu_prep(const uint16_t* xp, const float* xs, const uint32_t* qw,
+                                 const uint16_t* scales, const uint32_t* qzeros, uint16_t* out_xp,
+                                 float* out_xs, const float* bias, size_t M, size_t F, size_t K, int group,
+                                 size_t Mp, void* stream);
 
 int snx_k_i8_gemm(const int8_t* A, const int8_t* W, const float* sA, const float* sW,
                   int32_t* c_i32, uint16_t* out_bf16, const float* bias, size_t M, size_t N,

@@ -80,6 +80,8 @@ EXPORTS = {
                                                 _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul": (C.c_int, [_vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w4a16_swiglu": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, C.c_int, _vp]),
+    "SNEPPX_qlinear_w4a16_mlp": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, _sz, _sz,
+                                           _sz, _sz, C.c_int, _vp]),
     "SNEPPX_qlinear_silu_mul_quant_int8": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_dev_quantize_int8_channel_bf16": (C.c_int, [_vp, _vp, _vp, _sz, _sz, _vp]),
     "SNEPPX_qlinear_w8a8_i8": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _sz, _sz, _sz, _vp]),
@@ -410,6 +412,20 @@ class Library:
         self.check(self.fn["SNEPPX_qlinear_w4a16_swiglu"](
             _ptr(x), _ptr(qweight), _ptr(scales), _ptr(qzeros), _bias_ptr(bias, 2 * F, out), _ptr(out), M, F, K, group,
             self._stream(stream)), "qlinear_w4a16_swiglu")
+
+    def qlinear_w4a16_mlp(self, x, gate_up, down, y, group, stream=None, gu_bias=None, dn_bias=None):
+        """y [M][N] = down(silu(x . Wg^T) * (x . Wu^T)): gate_up = (qweight [2F][H/8],
+        scales, qzeros) of the stacked gate/up projection, down = (qweight [N][F/8],
+        scales, qzeros)."""
+        M, H = x.shape
+        gq, gs, gz = gate_up
+        dq, ds, dz = down
+        F = gq.shape[0] // 2
+        N = dq.shape[0]
+        ydt = SNEPPX_FLOAT32 if y.dtype == torch.float32 else SNEPPX_BFLOAT16
+        self.check(self.fn["SNEPPX_qlinear_w4a16_mlp"](
+            _ptr(x), _ptr(gq), _ptr(gs), _ptr(gz), _bias_ptr(gu_bias, 2 * F, y), _ptr(dq), _ptr(ds), _ptr(dz),
+            _bias_ptr(dn_bias, N, y), _ptr(y), ydt, M, H, F, N, group, self._stream(stream)), "qlinear_w4a16_mlp")
 
     def qlinear_silu_mul(self, gate_up, out, stream=None):
         T, F2 = gate_up.shape
