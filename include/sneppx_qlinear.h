@@ -125,7 +125,9 @@ int SNEPPX_qlinear_w4a16(const uint16_t* x, const uint32_t* qweight, const uint1
  * Same arguments, dispatch and results (bit-identical) as
  * SNEPPX_qlinear_w4a16, with one exception: where the allocating entry point
  * splits the prefill GEMM's K into spans (few output tiles, e.g. one GPU's
- * tensor-parallel QKV shard), this one runs that GEMM whole-K, the same
+ * tensor-parallel QKV shard, or the tiles past the last full round of CUs,
+ * e.g. the Llama-3-8B QKV projection at 1849 tokens), this one runs that
+ * GEMM whole-K, the same
  * product with another fp32 summation order, so a bf16 output can differ
  * in its last bit.  The scratch the split-K decode and the prefill
  * GEMM need (fp32 partials, prepared activations) comes from one static
