@@ -38,6 +38,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t brsrc(const void* p) {
 __device__ __forceinline__ void bload_lds(__amdgpu_buffer_rsrc_t r, void* dst, int bytes, uint32_t voff, uint32_t soff) {
     if (bytes == 16)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 16, voff, soff, 0, 0);
+    else if (bytes == 12)   // lane l's 12 bytes land at dst + 16 l (a 16-byte slot, its last 4 bytes untouched)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 12, voff, soff, 0, 0);
     else
         __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)dst, 4, voff, soff, 0, 0);
 }
@@ -480,7 +482,7 @@ __global__ void __launch_bounds__(512) k_mx8_tiled(const uint8_t* __restrict__ A
                                                    void* __restrict__ out, int M, int N, int K,
                                                    int tiles_m, int tiles_n) {
     constexpr int FM = 4;
-    constexpr int RB = 128 * EB / 8, NCH = RB / 16;      // bytes and chunks of a row per stage
+    constexpr int RB = 128 * EB / 8;                     // bytes of a row per stage
     extern __shared__ __attribute__((aligned(16))) int8_t lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -493,22 +495,22 @@ __global__ void __launch_bounds__(512) k_mx8_tiled(const uint8_t* __restrict__ A
     const int m0 = tm * TBM, n0 = tn * TBN;
     const uint32_t KB = (uint32_t)K * EB / 8, KS = (uint32_t)K / 32;   // code and scale bytes per row
 
-    // LDS slot lslot of row r holds chunk lslot ^ swz(r); padding slots of an
-    // fp6 row (chunk >= 6) repeat chunk c - 4 of the same row
+    // LDS slot lslot (16 bytes) of row r holds piece lslot ^ swz(r) of the
+    // row's stage bytes: 16-byte chunks of an fp8 row, 12-byte pieces of an
+    // fp6 row (8 x 12 = its 96 bytes; a 12-byte load fills the first 12
+    // bytes of each lane's 16-byte slot), so the stage streams exactly the
+    // rows' bytes
+    constexpr uint32_t PB = EB == 8 ? 16u : 12u;         // bytes per piece
     const int lrow = lane >> 3, lslot = lane & 7;
     uint32_t ga[4], gw[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int row = (8 * i + wave) * 8 + lrow;
         const int gr = m0 + row < M ? m0 + row : M - 1;
-        int c = lslot ^ swz(row);
-        c = c < NCH ? c : c - 4;
-        ga[i] = (uint32_t)gr * KB + (uint32_t)c * 16u;
+        ga[i] = (uint32_t)gr * KB + (uint32_t)(lslot ^ swz(row)) * PB;
         const int wr = row < TBN ? row : TBN - 1;
         const int gn = n0 + wr < N ? n0 + wr : N - 1;
-        int cw = lslot ^ swz(wr);
-        cw = cw < NCH ? cw : cw - 4;
-        gw[i] = (uint32_t)gn * KB + (uint32_t)cw * 16u;
+        gw[i] = (uint32_t)gn * KB + (uint32_t)(lslot ^ swz(wr)) * PB;
     }
     // scale dword of tile row d = 64 wave + lane (A rows, then W rows; d >= 480 repeats row 479)
     uint32_t gs;
@@ -529,10 +531,10 @@ __global__ void __launch_bounds__(512) k_mx8_tiled(const uint8_t* __restrict__ A
         int8_t* base = lds + buf * MX8_STAGE;
         const uint32_t k0 = (uint32_t)kt * RB;
 #pragma unroll
-        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
+        for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, PB, ga[i], k0);
 #pragma unroll
-        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
-        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
+        for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, PB, gw[i], k0);
+        if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, PB, gw[3], k0);
         // wave-uniform operand choice (waves 0-3 hold A rows, 4-7 W rows)
         if (wave < 4)
             bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs, 4u * (uint32_t)kt);
@@ -554,20 +556,17 @@ __global__ void __launch_bounds__(512) k_mx8_tiled(const uint8_t* __restrict__ A
     const int nk = K / 128;
 
     // lane group q's operand: fp8 chunks q and q + 4 of the row; fp6 block q
+    // (bytes [24 q, 24 q + 24) of the row = its pieces 2 q and 2 q + 1)
     auto frag = [&](const int8_t* row) -> i32x8 {
         if (EB == 8) {
             const i32x4 lo = lds16(row + ((q ^ sw) << 4));
             const i32x4 hi = lds16(row + (((q + 4) ^ sw) << 4));
             return i32x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         } else {
-            typedef int i32x2 __attribute__((ext_vector_type(2)));
-            i32x2 p[3];
-#pragma unroll
-            for (int j = 0; j < 3; j++) {
-                const int byte = 24 * q + 8 * j;
-                p[j] = *reinterpret_cast<const i32x2*>(row + ((((byte >> 4) ^ sw) << 4) | (byte & 15)));
-            }
-            return i32x8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], 0, 0};
+            typedef int i32x3 __attribute__((ext_vector_type(3)));
+            const i32x3 lo = *reinterpret_cast<const i32x3*>(row + (((2 * q) ^ sw) << 4));
+            const i32x3 hi = *reinterpret_cast<const i32x3*>(row + (((2 * q + 1) ^ sw) << 4));
+            return i32x8{lo[0], lo[1], lo[2], hi[0], hi[1], hi[2], 0, 0};
         }
     };
 
