@@ -325,7 +325,11 @@ constexpr int MXS_STAGE = TLDS_STAGE + MXS_ROWS * 8;
 
 __device__ __forceinline__ int e8m0_of(int8_t s) { return s < -127 ? 0 : (int)s + 127; }
 
-template <bool YF32>
+// PT (one exponent per operand, NVFP4's default): sA[0] + sW[0] split as
+// ceil / floor of its half (each at least -127), as k_mx_expand_scales
+// writes it into every block, and passed to every MFMA as a constant
+// instead of being staged per k-step.
+template <bool YF32, bool PT = false>
 __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__ A,
                                                      const int8_t* __restrict__ sA,
                                                      const uint8_t* __restrict__ W,
@@ -382,9 +386,17 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
 #pragma unroll
         for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
         if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
-        bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs[0], kt * 8);
-        if (wave < 7) bload_lds(rsw, base + TLDS_STAGE + (wave + 8) * 256, 4, gs[1], kt * 8);
+        if (!PT) {
+            bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs[0], kt * 8);
+            if (wave < 7) bload_lds(rsw, base + TLDS_STAGE + (wave + 8) * 256, 4, gs[1], kt * 8);
+        }
     };
+    int pta = 0, ptw = 0;
+    if (PT) {
+        const int t = (int)sA[0] + (int)sW[0];
+        pta = e8m0_of((int8_t)max(t - (t >> 1), -127));
+        ptw = e8m0_of((int8_t)max(t >> 1, -127));
+    }
 
     f32x4 acc[FM][TFN];
 #pragma unroll
@@ -418,13 +430,13 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
             for (int i = 0; i < FM; i++) {
                 const i32x4 v = lds16(ab + i * 16 * TBK + ((c ^ sw) << 4));
                 fa[i] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-                sca[i] = e8m0_of(sa_[i * 16 * 8 + c]);
+                sca[i] = PT ? pta : e8m0_of(sa_[i * 16 * 8 + c]);
             }
 #pragma unroll
             for (int j = 0; j < TFN; j++) {
                 const i32x4 v = lds16(wb + j * 16 * TBK + ((c ^ sw) << 4));
                 fw[j] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-                scw[j] = e8m0_of(sw_[j * 16 * 8 + c]);
+                scw[j] = PT ? ptw : e8m0_of(sw_[j * 16 * 8 + c]);
             }
 #pragma unroll
             for (int i = 0; i < FM; i++)
@@ -634,18 +646,18 @@ int launch_mx8_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const
     return snx_launch_check("k_mx8_tiled");
 }
 
-template <bool YF32>
+template <bool YF32, bool PT = false>
 int launch_mxfp4_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                        void* out, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
     const size_t lds = 2 * (size_t)MXS_STAGE;
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32>);
+    const void* kfn = reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32, PT>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("mxfp4 gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_mxfp4_tiled<YF32><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
+    k_mxfp4_tiled<YF32, PT><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
     return snx_launch_check("k_mxfp4_tiled");
 }
 
@@ -1275,6 +1287,17 @@ int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W,
     }
     if (y_f32) return launch_mxfp4_tiled<true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
     return launch_mxfp4_tiled<false>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+}
+
+// the same kernel on E2M1 operands with one exponent each (sA[0], sW[0])
+int snx_k_mxfp4_gemm_tiled_pt(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                              void* out, int y_f32, size_t M, size_t N, size_t K, void* st) {
+    if (K % 256 != 0 || (uint64_t)M * (K / 2) >= (1ull << 32) || (uint64_t)N * (K / 2) >= (1ull << 32)) {
+        snx_set_error("mxfp4 gemm: tiled kernel needs K %% 256 == 0 and operands below 4 GiB");
+        return -1;
+    }
+    if (y_f32) return launch_mxfp4_tiled<true, true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    return launch_mxfp4_tiled<false, true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
 }
 
 int snx_k_mx8_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,

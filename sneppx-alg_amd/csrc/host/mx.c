@@ -245,6 +245,13 @@ int SNEPPX_qlinear_mx_gemm_bs(const uint8_t* A, const int8_t* sA, const uint8_t*
     REQUIRE(A && sA && W && sW && out, "%s: NULL pointer", who);
     REQUIRE(M && N && K, "%s: empty shape", who);
     REQUIRE(K % 32 == 0, "%s: K=%zu must be a multiple of 32", who, K);
+    if (bs == 0 && ef == SNEPPX_MXFP4_E2M1 && K % 256 == 0 && M >= 128 && N >= 128) {
+        /* E2M1 with one exponent per operand (NVFP4): the tiled kernel splits
+         * the two exponents itself and takes them as constant block scales */
+        if (mx_gemm_check(who, A, sA, W, sW, ef, out, out_dtype, M, N, K)) return -1;
+        snx_clear_error();
+        return snx_k_mxfp4_gemm_tiled_pt(A, sA, W, sW, out, out_dtype == SNEPPX_FLOAT32, M, N, K, stream);
+    }
     snx_clear_error();
     const size_t kb = K / 32, ab = (M * kb + 255) & ~(size_t)255;
     int8_t* ws = (int8_t*)snx_workspace(ab + N * kb, 1, stream);

@@ -86,6 +86,10 @@ int snx_k_mxfp4_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const
 /* LDS-staged MXFP4 GEMM (256 x 224 tiles): K % 256 == 0, 4-byte aligned scales */
 int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                            void* out, int y_f32, size_t M, size_t N, size_t K, void* st);
+/* the same with one exponent per operand (sA[0], sW[0]; NVFP4's default):
+ * their sum split between the operands as k_mx_expand_scales splits it */
+int snx_k_mxfp4_gemm_tiled_pt(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
+                              void* out, int y_f32, size_t M, size_t N, size_t K, void* st);
 int snx_k_mx_dequant_tensor(const uint8_t* packed, float* y, size_t n, int s, int f, void* stream);
 /* reference MXFP8 blocks (f 0 e4m3, 1 e5m2) -> matrix-core-decodable codes and
  * exponents; *rounded (device, may be NULL) counts elements that rounded */
