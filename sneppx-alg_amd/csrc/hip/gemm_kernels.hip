@@ -164,6 +164,7 @@ constexpr int TLDS_A = TBM * TBK, TLDS_B = TBN * TBK, TLDS_STAGE = TLDS_A + TLDS
 
 __device__ __forceinline__ int swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 
+typedef int i32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ i32x4 lds16(const int8_t* p) { return *reinterpret_cast<const i32x4*>(p); }
 
 // fp8 (and the 16x16 int8 form): waves in 4 (M) x 2 (N), each 64 x 112 =
@@ -315,21 +316,50 @@ __global__ void __launch_bounds__(512) k_gemm_8w(const int8_t* __restrict__ A,
 // v_mfma_scale_f32_16x16x128_f8f6f4, staged like k_gemm_8w: 256 x 224 tiles,
 // 8 waves of 64 x 112, K stages of 128 bytes (256 elements) global -> LDS
 // with buffer_load_dwordx4 ... lds, double buffered.  Beside each stage sit the
-// stage's 8 scale bytes of every tile row (A rows then W rows, loaded with
-// 4-byte direct loads).  Lane (r16, q) takes 16-byte chunk 4h + q of its row
-// for k-step h - exactly one 32-element block, whose exponent is the lane's
-// MFMA scale operand (int8 s -> E8M0 s + 127).  The fp4 products are exact;
+// stage's 8 scale bytes of every tile row, as 4-byte direct loads (dword h of
+// a row: the exponents of its blocks 4h .. 4h + 3), ordered so that each lane
+// finds all the exponents of its fragments in 32 (A) + 64 (W) contiguous
+// bytes: A dword ((wm * 16 + r16) * 4 + i) * 2 + h holds row wm*64 + 16i + r16,
+// W dword ((wn * 16 + r16) * 8 + j) * 2 + h row wn*112 + 16j + r16 (j = 7
+// repeats j = 6, never read).  Lane (r16, q) takes 16-byte chunk 2q + h of
+// its row for k-step h (A and W alike: a permutation of the stage's k) -
+// exactly one 32-element block, whose exponent is the lane's MFMA scale
+// operand (int8 s -> E8M0 s + 127).  The lane's two exponents of a stage are
+// bytes 2(q % 2), +1 of dword q / 2: one byte permute puts them in bytes 0 and
+// 2, one packed 16-bit saturating subtract converts both, and the MFMA's scale
+// byte select (op_sel 0 / 2) takes each.  The fp4 products are exact;
 // accumulation is fp32.
-constexpr int MXS_ROWS = TBM + TBN;               // scale rows per stage
-constexpr int MXS_STAGE = TLDS_STAGE + MXS_ROWS * 8;
+constexpr int MXS_A = 4 * 16 * 4 * 2 * 4;         // bytes of A exponents per stage
+constexpr int MXS_STAGE = TLDS_STAGE + 2 * MXS_A;  // + as many for W (7 of 8 used)
 
 __device__ __forceinline__ int e8m0_of(int8_t s) { return s < -127 ? 0 : (int)s + 127; }
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+// the two exponent bytes of staged dwords {hi, lo} (bytes 4-7, 0-3) that sel
+// picks (e.g. 0x0C010C00: bytes 0, 1 of lo; 0x0C050C01: byte 1 of lo and of
+// hi) as E8M0 in bytes 0 and 2:
+// max(s, -127) + 127 = (s ^ 0x80) - 1, saturating at 0, per 16-bit half
+__device__ __forceinline__ int e8m0_pair(int hi, int lo, uint32_t sel) {
+    const uint32_t u = __builtin_amdgcn_perm((uint32_t)hi, (uint32_t)lo, sel) ^ 0x00800080u;
+    const u16x2 t = __builtin_elementwise_sub_sat(__builtin_bit_cast(u16x2, u), (u16x2){1, 1});
+    return __builtin_bit_cast(int, t);
+}
 
-// PT (one exponent per operand, NVFP4's default): sA[0] + sW[0] split as
-// ceil / floor of its half (each at least -127), as k_mx_expand_scales
-// writes it into every block, and passed to every MFMA as a constant
-// instead of being staged per k-step.
-template <bool YF32, bool PT = false>
+// SG picks where the exponents come from:
+//  0: one exponent per operand (NVFP4's default): sA[0] + sW[0] split as
+//     ceil / floor of its half (each at least -127), as k_mx_expand_scales
+//     writes it into every block, passed to every MFMA as a constant;
+//  1: staged beside each K stage, in the order above;
+//  4: (K a multiple of 1024) every fourth stage loads the next four stages'
+//     exponents, 32 bytes per row in two 16-byte direct loads, into one half
+//     of a double-buffered 32 KB area after the two stages.  One cache line
+//     per row per four stages instead of one per stage: the exponent loads
+//     touch as many lines as the code loads otherwise.  Granule (16 bytes:
+//     stages 2p, 2p + 1 of a row, dwords (stage, h)) order: A
+//     ((wm * 2 + p) * 4 + i) * 16 + r16, W ((wn * 2 + p) * 8 + j) * 16 + r16
+//     (j = 7 repeats j = 6, never read): the 16 rows one read instruction
+//     takes sit in 256 contiguous bytes, free of bank conflicts.
+constexpr int MXG_HALF = 2 * 512 * 16;   // bytes of one group of exponents (A, then W)
+template <bool YF32, int SG>
 __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__ A,
                                                      const int8_t* __restrict__ sA,
                                                      const uint8_t* __restrict__ W,
@@ -360,42 +390,54 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
         const int gn = n0 + wr < N ? n0 + wr : N - 1;
         gw[i] = (uint32_t)gn * KB + (uint32_t)((lslot ^ swz(wr)) * 16);
     }
-    // scale dwords of a stage: 2 per row x 480 rows = 15 wave instructions;
-    // wave w issues instructions w and w + 8 (the latter for w < 7)
-    // (instruction w covers rows 32 w .. 32 w + 31: all A rows for u = 0, all
-    // W rows for u = 1)
-    uint32_t gs[2];
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int d = 64 * (wave + 8 * u) + lane, row = d >> 1, half = d & 1;
-        if (row < TBM) {
-            const int gr = m0 + row < M ? m0 + row : M - 1;
-            gs[u] = (uint32_t)gr * KS + 4 * half;
-        } else {
-            const int r = row - TBM < TBN ? row - TBM : TBN - 1;
-            const int gn = n0 + r < N ? n0 + r : N - 1;
-            gs[u] = (uint32_t)gn * KS + 4 * half;
-        }
+    // SG 1: exponent dwords of a stage, 512 for A, 512 for W; SG 4: exponent
+    // granules of a group, as many; wave w's lanes load items 64 w .. 64 w + 63
+    // of each (the orders above)
+    uint32_t gs[2] = {0u, 0u};
+    if (SG == 1) {
+        const int d = 64 * wave + lane, h = d & 1;
+        const int ra = (d >> 7) * 64 + ((d >> 1) & 3) * 16 + ((d >> 3) & 15);
+        const int gr = m0 + ra < M ? m0 + ra : M - 1;
+        gs[0] = (uint32_t)gr * KS + 4 * h;
+        const int j = (d >> 1) & 7;
+        const int rw = (d >> 8) * 112 + (j < 7 ? j : 6) * 16 + ((d >> 4) & 15);
+        const int gn = n0 + rw < N ? n0 + rw : N - 1;
+        gs[1] = (uint32_t)gn * KS + 4 * h;
+    } else if (SG == 4) {
+        const int g = 64 * wave + lane;
+        const int ra = (g >> 7) * 64 + ((g >> 4) & 3) * 16 + (g & 15);
+        const int gr = m0 + ra < M ? m0 + ra : M - 1;
+        gs[0] = (uint32_t)gr * KS + 16 * ((g >> 6) & 1);
+        const int j = (g >> 4) & 7;
+        const int rw = (g >> 8) * 112 + (j < 7 ? j : 6) * 16 + (g & 15);
+        const int gn = n0 + rw < N ? n0 + rw : N - 1;
+        gs[1] = (uint32_t)gn * KS + 16 * ((g >> 7) & 1);
     }
+    constexpr int STG = SG == 1 ? MXS_STAGE : TLDS_STAGE;   // bytes per K stage
     const __amdgpu_buffer_rsrc_t ra = brsrc(A), rw = brsrc(W), rsa = brsrc(sA), rsw = brsrc(sW);
     auto dload = [&](int buf, int kt) {
-        int8_t* base = lds + buf * MXS_STAGE;
+        int8_t* base = lds + buf * STG;
         const uint32_t k0 = (uint32_t)kt * TBK;
 #pragma unroll
         for (int i = 0; i < 4; i++) bload_lds(ra, base + (8 * i + wave) * 1024, 16, ga[i], k0);
 #pragma unroll
         for (int i = 0; i < 3; i++) bload_lds(rw, base + TLDS_A + (8 * i + wave) * 1024, 16, gw[i], k0);
         if (wave < 4) bload_lds(rw, base + TLDS_A + (24 + wave) * 1024, 16, gw[3], k0);
-        if (!PT) {
+        if (SG == 1) {
             bload_lds(rsa, base + TLDS_STAGE + wave * 256, 4, gs[0], kt * 8);
-            if (wave < 7) bload_lds(rsw, base + TLDS_STAGE + (wave + 8) * 256, 4, gs[1], kt * 8);
+            bload_lds(rsw, base + TLDS_STAGE + MXS_A + wave * 256, 4, gs[1], kt * 8);
         }
     };
+    auto gload = [&](int grp) {   // SG 4: exponents of stages 4 grp .. 4 grp + 3
+        int8_t* base = lds + 2 * TLDS_STAGE + (grp & 1) * MXG_HALF;
+        bload_lds(rsa, base + wave * 1024, 16, gs[0], grp * 32);
+        bload_lds(rsw, base + MXG_HALF / 2 + wave * 1024, 16, gs[1], grp * 32);
+    };
     int pta = 0, ptw = 0;
-    if (PT) {
+    if (SG == 0) {
         const int t = (int)sA[0] + (int)sW[0];
-        pta = e8m0_of((int8_t)max(t - (t >> 1), -127));
-        ptw = e8m0_of((int8_t)max(t >> 1, -127));
+        pta = e8m0_of((int8_t)max(t - (t >> 1), -127)) * 0x10001;   // in bytes 0 and 2
+        ptw = e8m0_of((int8_t)max(t >> 1, -127)) * 0x10001;
     }
 
     f32x4 acc[FM][TFN];
@@ -407,43 +449,67 @@ __global__ void __launch_bounds__(512) k_mxfp4_tiled(const uint8_t* __restrict__
     const int sw = swz(r16);
     const int8_t* arow = lds + (wm * 64 + r16) * TBK;
     const int8_t* wrow = lds + TLDS_A + (wn * 112 + r16) * TBK;
-    const int8_t* srow_a = lds + TLDS_STAGE + (wm * 64 + r16) * 8;
-    const int8_t* srow_w = lds + TLDS_STAGE + (TBM + wn * 112 + r16) * 8;
+    // this lane's exponent dword (q / 2) of its first A / W row in a stage
+    const int8_t* srow_a = (SG == 1 ? lds + TLDS_STAGE + (wm * 16 + r16) * 32
+                                    : lds + 2 * TLDS_STAGE + wm * 2048 + r16 * 16) + 4 * (q >> 1);
+    const int8_t* srow_w = (SG == 1 ? lds + TLDS_STAGE + MXS_A + (wn * 16 + r16) * 64
+                                    : lds + 2 * TLDS_STAGE + MXG_HALF / 2 + wn * 4096 + r16 * 16) + 4 * (q >> 1);
+    const uint32_t psel = (q & 1) ? 0x0C030C02u : 0x0C010C00u;
     const int nk = K / (2 * TBK);
 
     dload(0, 0);
+    if (SG == 4) gload(0);
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
         __builtin_amdgcn_s_waitcnt(0x0070);   // this stage landed; earlier LDS reads done
         __syncthreads();
         dload(cur ^ 1, kt + 1 < nk ? kt + 1 : 0);   // last stage: stage 0 again, unused
-        const int8_t* ab = arow + cur * MXS_STAGE;
-        const int8_t* wb = wrow + cur * MXS_STAGE;
-        const int8_t* sa_ = srow_a + cur * MXS_STAGE;
-        const int8_t* sw_ = srow_w + cur * MXS_STAGE;
+        // the other half was last read in the previous group, before the barrier above
+        if (SG == 4 && (kt & 3) == 0 && kt + 4 < nk) gload((kt >> 2) + 1);
+        const int8_t* ab = arow + cur * STG;
+        const int8_t* wb = wrow + cur * STG;
+        // per fragment row, this lane's two exponents of the stage as E8M0 in bytes 0, 2
+        int ea[FM], ew[TFN];
+        if (SG == 0) {
+#pragma unroll
+            for (int i = 0; i < FM; i++) ea[i] = pta;
+#pragma unroll
+            for (int j = 0; j < TFN; j++) ew[j] = ptw;
+        } else {
+            // SG 4: group half, granule pair (kt / 2) % 2, stage kt % 2 within it
+            const int8_t* xa = SG == 4 ? srow_a + ((kt >> 2) & 1) * MXG_HALF + ((kt >> 1) & 1) * 1024 + (kt & 1) * 8
+                                       : srow_a + cur * STG;
+            const int8_t* xw = SG == 4 ? srow_w + ((kt >> 2) & 1) * MXG_HALF + ((kt >> 1) & 1) * 2048 + (kt & 1) * 8
+                                       : srow_w + cur * STG;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                ea[i] = e8m0_pair(0, *reinterpret_cast<const int*>(xa + (SG == 4 ? 256 : 8) * i), psel);
+#pragma unroll
+            for (int j = 0; j < TFN; j++)
+                ew[j] = e8m0_pair(0, *reinterpret_cast<const int*>(xw + (SG == 4 ? 256 : 8) * j), psel);
+        }
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const int c = 4 * h + q;
+            const int c = 2 * q + h;
             i32x8 fa[FM], fw[TFN];
-            int sca[FM], scw[TFN];
 #pragma unroll
             for (int i = 0; i < FM; i++) {
                 const i32x4 v = lds16(ab + i * 16 * TBK + ((c ^ sw) << 4));
                 fa[i] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-                sca[i] = PT ? pta : e8m0_of(sa_[i * 16 * 8 + c]);
             }
 #pragma unroll
             for (int j = 0; j < TFN; j++) {
                 const i32x4 v = lds16(wb + j * 16 * TBK + ((c ^ sw) << 4));
                 fw[j] = i32x8{v[0], v[1], v[2], v[3], 0, 0, 0, 0};
-                scw[j] = PT ? ptw : e8m0_of(sw_[j * 16 * 8 + c]);
             }
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
                 for (int j = 0; j < TFN; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-                        fa[i], fw[j], acc[i][j], 4, 4, 0, sca[i], 0, scw[j]);
+                    acc[i][j] = h == 0 ? __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                             fa[i], fw[j], acc[i][j], 4, 4, 0, ea[i], 0, ew[j])
+                                       : __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+                                             fa[i], fw[j], acc[i][j], 4, 4, 2, ea[i], 2, ew[j]);
         }
     }
     __builtin_amdgcn_s_waitcnt(0x0070);   // the last (unused) loads drain before exit
@@ -646,18 +712,19 @@ int launch_mx8_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const
     return snx_launch_check("k_mx8_tiled");
 }
 
-template <bool YF32, bool PT = false>
+template <bool YF32, int SG>
 int launch_mxfp4_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,
                        void* out, int M, int N, int K, hipStream_t st) {
     const int tiles_m = (M + TBM - 1) / TBM, tiles_n = (N + TBN - 1) / TBN;
-    const size_t lds = 2 * (size_t)MXS_STAGE;
+    const size_t lds = SG == 1 ? 2 * (size_t)MXS_STAGE
+                               : 2 * (size_t)TLDS_STAGE + (SG == 4 ? 2 * MXG_HALF : 0);
     static std::atomic<uint64_t> lds_done{0};   // > 64 KB of LDS per workgroup, per device
-    const void* kfn = reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32, PT>);
+    const void* kfn = reinterpret_cast<const void*>(&k_mxfp4_tiled<YF32, SG>);
     if (snx::lds_optin(kfn, (int)lds, lds_done) != hipSuccess) {
         snx_set_error("mxfp4 gemm: cannot reserve %zu bytes of LDS", lds);
         return -1;
     }
-    k_mxfp4_tiled<YF32, PT><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
+    k_mxfp4_tiled<YF32, SG><<<tiles_m * tiles_n, 512, lds, st>>>(A, sA, W, sW, out, M, N, K, tiles_m, tiles_n);
     return snx_launch_check("k_mxfp4_tiled");
 }
 
@@ -1285,8 +1352,12 @@ int snx_k_mxfp4_gemm_tiled(const uint8_t* A, const int8_t* sA, const uint8_t* W,
         snx_set_error("mxfp4 gemm: tiled kernel needs K %% 256 == 0 and operands below 4 GiB");
         return -1;
     }
-    if (y_f32) return launch_mxfp4_tiled<true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
-    return launch_mxfp4_tiled<false>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    if (K % 1024 == 0) {
+        if (y_f32) return launch_mxfp4_tiled<true, 4>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+        return launch_mxfp4_tiled<false, 4>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    }
+    if (y_f32) return launch_mxfp4_tiled<true, 1>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    return launch_mxfp4_tiled<false, 1>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
 }
 
 // the same kernel on E2M1 operands with one exponent each (sA[0], sW[0])
@@ -1296,8 +1367,8 @@ int snx_k_mxfp4_gemm_tiled_pt(const uint8_t* A, const int8_t* sA, const uint8_t*
         snx_set_error("mxfp4 gemm: tiled kernel needs K %% 256 == 0 and operands below 4 GiB");
         return -1;
     }
-    if (y_f32) return launch_mxfp4_tiled<true, true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
-    return launch_mxfp4_tiled<false, true>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    if (y_f32) return launch_mxfp4_tiled<true, 0>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
+    return launch_mxfp4_tiled<false, 0>(A, sA, W, sW, out, (int)M, (int)N, (int)K, S(st));
 }
 
 int snx_k_mx8_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W, const int8_t* sW,

@@ -91,7 +91,7 @@ def test_rejects_block_sizes_that_are_not_byte_aligned(lib):
 
 @pytest.mark.parametrize("M,N,K,out", [(128, 128, 64, "f32"), (300, 200, 512, "f32"), (1, 4096, 4096, "bf16"),
                                        (2048, 1024, 4096, "f32"), (257, 450, 768, "f32"),
-                                       (384, 448, 1024, "bf16")])
+                                       (384, 448, 1024, "bf16"), (300, 260, 3072, "bf16")])
 def test_mxfp4_gemm_against_dequantized_product(lib, M, N, K, out):
     print(f"[gpu] mxfp4 gemm M={M} N={N} K={K}", flush=True)
     rng = np.random.default_rng(M + N + K)
