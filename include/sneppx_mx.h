@@ -107,7 +107,10 @@ int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
  * (mx_formats.py:165-172, 199-203); a block of 32 r repeats each exponent for
  * its r pieces of 32.  Blocks that are no multiple of 32 (e.g. 16) return -1:
  * the matrix cores scale 32 elements with one exponent.  NVFP4 runs the
- * MXFP4 kernels (the same E2M1 codes).  The rewritten exponents go to the
+ * MXFP4 kernels (the same E2M1 codes).  E2M1 per tensor with K % 256 == 0
+ * and M, N >= 128 passes the two exponents to every MFMA as constant scales
+ * (the product's exponent split as ceil / floor of its half, each at least
+ * -127) and needs no workspace; other cases rewrite the exponents into the
  * calling thread's workspace (M + N rows of K/32 bytes). */
 int SNEPPX_qlinear_mx_gemm_bs(const uint8_t* A, const int8_t* sA, const uint8_t* W,
                               const int8_t* sW, SNEPPXMXFormat fmt, int block_size, void* out,

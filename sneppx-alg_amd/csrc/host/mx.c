@@ -223,11 +223,13 @@ int SNEPPX_qlinear_mx_gemm(const uint8_t* A, const int8_t* sA, const uint8_t* W,
 
 /* Any block the reference's quantize_mx takes (mx_formats.py:147-150: the
  * format's own, an override, or per tensor) whose scales the matrix cores
- * can apply exactly: per tensor, or a multiple of 32 elements.  The
- * exponents are rewritten into the block-32 form (k_mx_expand_scales, into
- * the calling thread's workspace) and the block-32 GEMM runs on the
- * operands' own codes: NVFP4's and MXFP4's E2M1 codes are the same, and with
- * K a multiple of the block every row's codes start on a byte. */
+ * can apply exactly: per tensor, or a multiple of 32 elements.  E2M1 per
+ * tensor on the tiled kernel's shapes takes the two exponents as constant
+ * scales; otherwise the exponents are rewritten into the block-32 form
+ * (k_mx_expand_scales, into the calling thread's workspace) and the block-32
+ * GEMM runs on the operands' own codes: NVFP4's and MXFP4's E2M1 codes are
+ * the same, and with K a multiple of the block every row's codes start on a
+ * byte. */
 int SNEPPX_qlinear_mx_gemm_bs(const uint8_t* A, const int8_t* sA, const uint8_t* W,
                               const int8_t* sW, SNEPPXMXFormat fmt, int block_size, void* out,
                               SNEPPXDtype out_dtype, size_t M, size_t N, size_t K,
