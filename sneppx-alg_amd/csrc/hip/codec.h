@@ -131,6 +131,14 @@ __device__ __forceinline__ uint16_t bf16_out(float f) {
     return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+// Two outputs in one v_cvt_pk_bf16_f32: lo in bits 0..15, hi in 16..31 (each
+// the value bf16_out gives).
+__device__ __forceinline__ uint32_t bf16x2_out(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
+}
+
 // SiLU(g) * u as the fused SwiGLU epilogue computes it: the exponential and
 // the reciprocal on the hardware's fast approximations (about 1 ulp each,
 // far below the bf16 rounding of the result).  Large negative g gives

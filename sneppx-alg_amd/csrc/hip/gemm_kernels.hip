@@ -1196,10 +1196,15 @@ __global__ void __launch_bounds__(512) k_gemm_8wp(const int8_t* __restrict__ A,
 #pragma unroll
                 for (int j = 0; j < TFN; j++)
 #pragma unroll
-                    for (int e = 0; e < 4; e++)
-                        ct[((i - 2 * p) * 16 + q * 4 + e) * PCROW + j * 16 + r16] =
-                            BIAS ? bf16_out((float)acc[i][j][e] * sa[e] * swv[j] + bv[j])
-                                 : bf16_out((float)acc[i][j][e] * sa[e] * swv[j]);
+                    for (int e = 0; e < 4; e += 2) {   // rows e, e + 1 in one conversion
+                        float v0 = (float)acc[i][j][e] * sa[e] * swv[j];
+                        float v1 = (float)acc[i][j][e + 1] * sa[e + 1] * swv[j];
+                        if (BIAS) v0 += bv[j], v1 += bv[j];
+                        const uint32_t pk = bf16x2_out(v0, v1);
+                        uint16_t* c0 = ct + ((i - 2 * p) * 16 + q * 4 + e) * PCROW + j * 16 + r16;
+                        c0[0] = (uint16_t)pk;
+                        c0[PCROW] = (uint16_t)(pk >> 16);
+                    }
             }
 #pragma unroll
             for (int c = 0; c < 7; c++) {     // 32 rows x 14 pieces of 16 B = 7 x 64
