@@ -2,8 +2,9 @@
 end_capture / graph_launch): every replay gives the eager bits, with eager
 work on the same stream and on the default stream between the replays.
 Covers the M = 1 W4A16 GEMV (full and ragged K), its GLU (gate/up +
-SwiGLU) form, the prepared act-order GEMV and the W8 GEMV, chained as a
-decode step chains them (one linear's output is the next one's input)."""
+SwiGLU) form, the decode MLP call (gate/up + SwiGLU, then down), the
+prepared act-order GEMV and the W8 GEMV, chained as a decode step chains them (one linear's output is the
+next one's input)."""
 import numpy as np
 import pytest
 import torch
@@ -23,7 +24,7 @@ def _w4(lib, N, K, seed):
 
 
 def test_decode_step_graph_replays_match_eager(lib):
-    print("[gpu] graph: W4 GEMV, GLU, ragged-K GEMV, act-order, W8 GEMV chained; 4 replays", flush=True)
+    print("[gpu] graph: W4 GEMV, GLU, ragged-K GEMV, act-order, W8 GEMV, MLP call chained; 4 replays", flush=True)
     H, F, N2, NG, N8 = 4096, 1792, 3072, 2048, 1000
     s = torch.cuda.Stream()
     st = s.cuda_stream
@@ -46,13 +47,15 @@ def test_decode_step_graph_replays_match_eager(lib):
         q8 = torch.empty((N8, NG), dtype=torch.int8, device=DEV)
         s8 = torch.empty(N8, device=DEV)
         lib.dev_quantize_int8_channel(w8, q8, s8)
+        w_dn = _w4(lib, H, F, 6)                # the MLP's down projection F -> H
         x = torch.randn((1, H), device=DEV).to(torch.bfloat16)
         outs = [torch.empty((1, H), dtype=torch.bfloat16, device=DEV),
                 torch.empty((1, F), dtype=torch.bfloat16, device=DEV),
                 torch.empty((1, N2), dtype=torch.bfloat16, device=DEV),
                 torch.empty((1, NG), device=DEV),
-                torch.empty((1, N8), device=DEV)]
-        y1, h, y2, y3, y4 = outs
+                torch.empty((1, N8), device=DEV),
+                torch.empty((1, H), dtype=torch.bfloat16, device=DEV)]
+        y1, h, y2, y3, y4, y5 = outs
 
         def step():
             lib.qlinear_w4a16(x, w_a[0], w_a[1], w_a[2], None, H // 128, y1, 128, stream=st)
@@ -60,6 +63,7 @@ def test_decode_step_graph_replays_match_eager(lib):
             lib.qlinear_w4a16(h, w_b[0], w_b[1], w_b[2], None, F // 128, y2, 128, stream=st)
             lib.qlinear_w4a16_actorder(y2, qs, sc_g, None, perm, y3, 128, stream=st)
             lib.qlinear_w8_gemv(y3, q8, s8, y4, stream=st)
+            lib.qlinear_w4a16_mlp(y1, w_gu, w_dn, y5, 128, stream=st)
 
         step()
         s.synchronize()

@@ -35,7 +35,12 @@ def _dev_w4(lib, N, K, seed, sym=False):
     (600, 1024, 2048, 256, False, False, "bf16"),     # few down tiles: the down GEMM in K spans
     (257, 1024, 1024, 768, False, True, "f32"),       # one row past a tile
     (8, 512, 384, 256, False, True, "bf16"),          # decode rows: the two calls
-    (1, 4096, 1792, 4096, False, False, "bf16"),      # one token (a TP=8 shard's MLP): the two calls
+    (1, 4096, 1792, 4096, False, False, "bf16"),      # one token, a TP=8 shard's MLP (ragged K of down)
+    (1, 4096, 14336, 4096, False, True, "bf16"),      # one token, the C5 MLP, biases on both
+    (1, 4096, 14336, 4096, True, False, "bf16"),      # the same without zero words
+    (1, 8192, 2816, 1024, False, True, "bf16"),       # H = 8192, ragged F
+    (1, 4096, 2048, 300, True, True, "bf16"),         # few down rows
+    (1, 4096, 1792, 4096, False, True, "f32"),        # fp32 output
 ])
 def test_mlp_equals_swiglu_then_down(lib, M, H, F, N, sym, bias, out):
     print(f"[gpu] w4a16 mlp M={M} H={H} F={F} N={N} sym={sym} bias={bias} out={out}", flush=True)
@@ -57,9 +62,11 @@ def test_mlp_equals_swiglu_then_down(lib, M, H, F, N, sym, bias, out):
     iv = torch.int32 if out == "f32" else torch.int16
     assert torch.equal(y.view(iv), y2.view(iv))
     # again with the workspaces warm: same bits
-    lib.qlinear_w4a16_mlp(x, gu, dn, y, 128, gu_bias=gb, dn_bias=db)
-    torch.cuda.synchronize()
-    assert torch.equal(y.view(iv), y2.view(iv))
+    for _ in range(3):
+        y.zero_()
+        lib.qlinear_w4a16_mlp(x, gu, dn, y, 128, gu_bias=gb, dn_bias=db)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(iv), y2.view(iv))
 
 
 def test_mlp_against_oracle(lib, oracle):
