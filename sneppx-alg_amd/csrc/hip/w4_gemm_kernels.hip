@@ -46,36 +46,50 @@ constexpr int GLDS_A = GBM * GBK * 2;           // 32 KB of bf16 activations
 constexpr int GLDS_B = GBN * GBK / 2;           // 16 KB of packed weights
 
 // ---------------------------------------------------------------- prep pass
-// One thread per 8 columns.  K % 128 == 0, so the 16 threads of one
-// 128-column step are 16 consecutive lanes.
+// One thread per 8 columns of PREP_ITEMS items: thread t of block b takes
+// items 1024 b + 256 i + t (i < 4), all four loads issued before the first
+// is used (with one load per thread the pass is bound by load latency, not
+// by its bytes).  K % 128 == 0, so the 16 items of one 128-column step are
+// 16 consecutive lanes.
+constexpr int PREP_ITEMS = 4;
+
 __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ xp,
                                                    float* __restrict__ xs, int K, int Mp,
                                                    size_t items) {
-    const size_t it = (size_t)blockIdx.x * 256 + threadIdx.x;
-    const bool live = it < items;
-    const size_t itc = live ? it : items - 1;
+    const size_t base = (size_t)blockIdx.x * (256 * PREP_ITEMS) + threadIdx.x;
     const int k8n = K >> 3;
-    const int m = (int)(itc / (size_t)k8n);
-    const int k8 = (int)(itc - (size_t)m * k8n);
-    const u32x4 v = *reinterpret_cast<const u32x4*>(x + itc * 8);
-    u32x4 p;
-    p[0] = __builtin_amdgcn_perm(v[2], v[0], 0x05040100u);
-    p[1] = __builtin_amdgcn_perm(v[2], v[0], 0x07060302u);
-    p[2] = __builtin_amdgcn_perm(v[3], v[1], 0x05040100u);
-    p[3] = __builtin_amdgcn_perm(v[3], v[1], 0x07060302u);
-    // input chunk 8 h + s of its 128-column step goes to chunk 2 s + h
-    const int jin = k8 & 15, jout = 2 * (jin & 7) + (jin >> 3);
-    if (live) *reinterpret_cast<u32x4*>(xp + (itc - jin + jout) * 8) = p;
-    float sum = 0.0f;
+    u32x4 v[PREP_ITEMS];
 #pragma unroll
-    for (int e = 0; e < 4; e++)
-        sum += __builtin_bit_cast(float, v[e] << 16) + __builtin_bit_cast(float, v[e] & 0xFFFF0000u);
-    sum += __shfl_xor(sum, 8);
-    sum += __shfl_xor(sum, 4);
-    sum += __shfl_xor(sum, 2);
-    sum += __shfl_xor(sum, 1);
-    if (live && (k8 & 15) == 0) xs[(size_t)(k8 >> 4) * Mp + m] = sum;
+    for (int i = 0; i < PREP_ITEMS; i++) {
+        const size_t it = base + 256 * i;
+        v[i] = *reinterpret_cast<const u32x4*>(x + (it < items ? it : items - 1) * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < PREP_ITEMS; i++) {
+        const size_t it = base + 256 * i;
+        const bool live = it < items;
+        const size_t itc = live ? it : items - 1;
+        const int m = (int)(itc / (size_t)k8n);
+        const int k8 = (int)(itc - (size_t)m * k8n);
+        u32x4 p;
+        p[0] = __builtin_amdgcn_perm(v[i][2], v[i][0], 0x05040100u);
+        p[1] = __builtin_amdgcn_perm(v[i][2], v[i][0], 0x07060302u);
+        p[2] = __builtin_amdgcn_perm(v[i][3], v[i][1], 0x05040100u);
+        p[3] = __builtin_amdgcn_perm(v[i][3], v[i][1], 0x07060302u);
+        // input chunk 8 h + s of its 128-column step goes to chunk 2 s + h
+        const int jin = k8 & 15, jout = 2 * (jin & 7) + (jin >> 3);
+        if (live) *reinterpret_cast<u32x4*>(xp + (itc - jin + jout) * 8) = p;
+        float sum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            sum += __builtin_bit_cast(float, v[i][e] << 16) + __builtin_bit_cast(float, v[i][e] & 0xFFFF0000u);
+        sum += __shfl_xor(sum, 8);
+        sum += __shfl_xor(sum, 4);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 1);
+        if (live && (k8 & 15) == 0) xs[(size_t)(k8 >> 4) * Mp + m] = sum;
+    }
 }
 
 // ----------------------------------------------------------------- the GEMM
@@ -770,7 +784,8 @@ int snx_w4a16_gemm_ok(size_t M, size_t N, size_t K, int group) {
 int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t K, size_t Mp,
                     void* st) {
     const size_t items = M * (K / 8);
-    k_w4_prep_x<<<(unsigned)((items + 255) / 256), 256, 0, S(st)>>>(x, xp, xs, (int)K, (int)Mp, items);
+    const size_t per = 256 * PREP_ITEMS;
+    k_w4_prep_x<<<(unsigned)((items + per - 1) / per), 256, 0, S(st)>>>(x, xp, xs, (int)K, (int)Mp, items);
     return snx_launch_check("k_w4_prep_x");
 }
 
