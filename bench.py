@@ -382,12 +382,13 @@ def bench_w8a8(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
         lib.dev_quantize_int8_channel(w32, W, sW)
         calls = [lambda: lib.qlinear_w8a8_i8(A, sA, W, sW, out, stream=st)]
     del a32, w32
-    total, mean_launch, _ = timer.run(calls, steps, warmup)
+    with ClockSampler() as clk:
+        total, mean_launch, _ = timer.run(calls, steps, warmup)
     ops = 2 * M * N * K
     host = {"A": A[:CPU_ROWS].cpu().numpy(), "W": W.cpu().numpy(), "sA": sA[:CPU_ROWS].cpu().numpy(),
             "sW": sW.cpu().numpy(), "M": M}
     return {"ops": ops, "ms_per_step": total / steps, "tops": ops / (total / steps) / 1e9,
-            "tops_kernel": ops / mean_launch / 1e9, "host": host}
+            "tops_kernel": ops / mean_launch / 1e9, "host": host, "sclk_dpm_mhz_median": clk.median()}
 
 
 def bench_w8a8_dyn(lib, timer, torch, M, N, K, steps, warmup, fp8=False):
@@ -543,7 +544,8 @@ def bench_chain(lib, timer, torch, steps, warmup, tp=1):
         lin("o", attn, y_o)
         mlp(y_o, y_d)                      # gate/up + SiLU(gate) * up -> down
 
-    total, _, _ = timer.run([layer], steps, warmup)
+    with ClockSampler() as clk:
+        total, _, _ = timer.run([layer], steps, warmup)
     per = {}
     for name, fn in (("qkv", lambda: lin("qkv", x, y_qkv)), ("o", lambda: lin("o", attn, y_o)),
                      ("gate_up+swiglu", lambda: gate_up_swiglu(y_o, act)),
@@ -563,6 +565,7 @@ def bench_chain(lib, timer, torch, steps, warmup, tp=1):
     host = {"x": _u16(x[:2 * CPU_ROWS]), "attn": _u16(attn[:2 * CPU_ROWS]), "shapes": shapes,
             "w": {name: (_u32(qw), _u16(sc), _u32(qz)) for name, (qw, sc, qz, G) in ws.items()}}
     return {"T": T, "chunk_lens": lens, "flops": flops, "ms_per_step": total / steps,
+            "sclk_dpm_mhz_median": clk.median(),
             "tflops": flops / (total / steps) / 1e9, "per_linear": per, "host": host}
 
 
@@ -981,6 +984,38 @@ def _gpu_sclk_mhz():
     return None
 
 
+class ClockSampler:
+    """Median shader clock level (MHz) the driver reports in sysfs
+    (pp_dpm_sclk, the active DPM level) over a timed region, sampled every
+    2 ms from a host thread; None where sysfs gives no reading.  The level
+    is the clock requested, not the effective clock under the power limit,
+    which the SQ counters give (CU-busy cycles / kernel time)."""
+
+    def __enter__(self):
+        import threading
+        self.samples, self._stop = [], False
+
+        def run():
+            while not self._stop:
+                c = _gpu_sclk_mhz()
+                if c:
+                    self.samples.append(c)
+                time.sleep(0.002)
+        self._t = threading.Thread(target=run, daemon=True)
+        self._t.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop = True
+        self._t.join()
+
+    def median(self):
+        if not self.samples:
+            return None
+        v = sorted(self.samples)
+        return v[len(v) // 2]
+
+
 def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -1076,7 +1111,7 @@ def main():
                       "value": round(r["tflops"], 1), "unit": "TFLOP/s",
                       "frac_of_peak": round(r["tflops"] / BF16_PEAK_TFLOPS, 4),
                       "ms_per_step": round(r["ms_per_step"], 4), "steps": 10, "warmup": 30,
-                      "per_linear": r["per_linear"]})
+                      "sclk_dpm_mhz_median": r["sclk_dpm_mhz_median"], "per_linear": r["per_linear"]})
         cpu_jobs.append((extra[-1], "chain", dict(r["host"], T=r["T"], flops=r["flops"])))
         print(f"[bench] C5 chain T={r['T']}: {r['ms_per_step'] * 1e3:.0f} us, {r['tflops']:.0f} TFLOP/s",
               file=sys.stderr, flush=True)
@@ -1087,7 +1122,8 @@ def main():
             extra.append({"workload": f"C4 W8A8 {'fp8 e4m3' if fp8 else 'int8'} GEMM M=2048 N=14336 K=4096",
                           "value": round(r["tops"], 1), "unit": "TOPS",
                           "frac_of_peak": round(r["tops"] / peak, 4), "ms_per_step": round(r["ms_per_step"], 4),
-                          "kernel_tops": round(r["tops_kernel"], 1), "steps": GEMM_STEPS, "warmup": GEMM_WARMUP})
+                          "kernel_tops": round(r["tops_kernel"], 1), "steps": GEMM_STEPS, "warmup": GEMM_WARMUP,
+                          "sclk_dpm_mhz_median": r["sclk_dpm_mhz_median"]})
             gemm[kind] = dict(r, peak=peak, line=extra[-1])
             cpu_jobs.append((extra[-1], "fp8" if fp8 else "i8", r["host"]))
             print(f"[bench] C4 W8A8 {kind} GEMM M=2048 N=14336 K=4096: {r['tops']:.0f} TOPS "
@@ -1210,6 +1246,7 @@ def roofline_gemm(gemm):
                      "kernel_event_pair_tops": round(g["tops_kernel"], 1),
                      "launch_us": round(g["ms_per_step"] * 1e3, 2),
                      "traffic": load_traffic(f"k_gemm_8wp<{kind}>"),
+                     "sclk_dpm_mhz_median": g.get("sclk_dpm_mhz_median"),
                      "cpu_baseline": g["line"].get("cpu_baseline")}
     return out
 
