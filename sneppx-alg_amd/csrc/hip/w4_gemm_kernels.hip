@@ -56,30 +56,31 @@ constexpr int PREP_ITEMS = 4;
 __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ x,
                                                    uint16_t* __restrict__ xp,
                                                    float* __restrict__ xs, int K, int Mp,
-                                                   size_t items) {
-    const size_t base = (size_t)blockIdx.x * (256 * PREP_ITEMS) + threadIdx.x;
-    const int k8n = K >> 3;
+                                                   uint32_t items) {
+    // item indices in 32 bits (the host keeps items below 2^31)
+    const uint32_t base = blockIdx.x * (256u * PREP_ITEMS) + threadIdx.x;
+    const uint32_t k8n = (uint32_t)K >> 3;
     u32x4 v[PREP_ITEMS];
 #pragma unroll
     for (int i = 0; i < PREP_ITEMS; i++) {
-        const size_t it = base + 256 * i;
-        v[i] = *reinterpret_cast<const u32x4*>(x + (it < items ? it : items - 1) * 8);
+        const uint32_t it = base + 256u * i;
+        v[i] = *reinterpret_cast<const u32x4*>(x + (size_t)(it < items ? it : items - 1) * 8);
     }
 #pragma unroll
     for (int i = 0; i < PREP_ITEMS; i++) {
-        const size_t it = base + 256 * i;
+        const uint32_t it = base + 256u * i;
         const bool live = it < items;
-        const size_t itc = live ? it : items - 1;
-        const int m = (int)(itc / (size_t)k8n);
-        const int k8 = (int)(itc - (size_t)m * k8n);
+        const uint32_t itc = live ? it : items - 1;
+        const uint32_t m = itc / k8n;
+        const uint32_t k8 = itc - m * k8n;
         u32x4 p;
         p[0] = __builtin_amdgcn_perm(v[i][2], v[i][0], 0x05040100u);
         p[1] = __builtin_amdgcn_perm(v[i][2], v[i][0], 0x07060302u);
         p[2] = __builtin_amdgcn_perm(v[i][3], v[i][1], 0x05040100u);
         p[3] = __builtin_amdgcn_perm(v[i][3], v[i][1], 0x07060302u);
         // input chunk 8 h + s of its 128-column step goes to chunk 2 s + h
-        const int jin = k8 & 15, jout = 2 * (jin & 7) + (jin >> 3);
-        if (live) *reinterpret_cast<u32x4*>(xp + (itc - jin + jout) * 8) = p;
+        const uint32_t jin = k8 & 15, jout = 2 * (jin & 7) + (jin >> 3);
+        if (live) *reinterpret_cast<u32x4*>(xp + (size_t)(itc - jin + jout) * 8) = p;
         float sum = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; e++)
@@ -88,7 +89,7 @@ __global__ void __launch_bounds__(256) k_w4_prep_x(const uint16_t* __restrict__ 
         sum += __shfl_xor(sum, 4);
         sum += __shfl_xor(sum, 2);
         sum += __shfl_xor(sum, 1);
-        if (live && (k8 & 15) == 0) xs[(size_t)(k8 >> 4) * Mp + m] = sum;
+        if (live && (k8 & 15) == 0) xs[(size_t)(k8 >> 4) * (uint32_t)Mp + m] = sum;
     }
 }
 
@@ -785,7 +786,12 @@ int snx_k_w4_prep_x(const uint16_t* x, uint16_t* xp, float* xs, size_t M, size_t
                     void* st) {
     const size_t items = M * (K / 8);
     const size_t per = 256 * PREP_ITEMS;
-    k_w4_prep_x<<<(unsigned)((items + per - 1) / per), 256, 0, S(st)>>>(x, xp, xs, (int)K, (int)Mp, items);
+    if (items == 0 || items >= (1ull << 31)) {
+        snx_set_error("w4a16 activation pass: %zu x %zu activations out of range", M, K);
+        return -1;
+    }
+    k_w4_prep_x<<<(unsigned)((items + per - 1) / per), 256, 0, S(st)>>>(x, xp, xs, (int)K, (int)Mp,
+                                                                         (uint32_t)items);
     return snx_launch_check("k_w4_prep_x");
 }
 
